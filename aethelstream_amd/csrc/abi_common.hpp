@@ -1,0 +1,34 @@
+// abi_common.hpp - host-side helpers shared by the extern "C" entry points:
+// status codes, the per-thread error message, and nf4s_tensor validation
+// mirroring shard_engine/src/nf4.rs:43-57.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include "../../include/nf4stream.h"
+
+namespace nf4s {
+
+// Formats the message returned by nf4s_last_error_message() and returns rc.
+int32_t fail(int32_t rc, const char *fmt, ...);
+
+inline int32_t clear_ok() { return NF4S_OK; }
+
+inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Launch status of the kernel just enqueued.
+int32_t check_launch(const char *what);
+
+inline bool aligned(const void *p, uintptr_t a) {
+  return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0;
+}
+
+// Validates `t` for reading n elements: the two MalformedIndex checks of
+// shard_engine/src/nf4.rs:46-57 (same order, same message text), plus the
+// pointer and double-quant fields.
+int32_t validate_tensor(const nf4s_tensor *t, int64_t n);
+
+}  // namespace nf4s

@@ -1,0 +1,354 @@
+// nf4_codec.hip - NF4 quantize, double-quant encode and dequant kernels for
+// gfx950, with their extern "C" entry points.
+//
+// Dequant is HBM-bound (2.52 B per element with double-quant, bf16 out): the
+// fast kernel moves 16 B of packed nibbles per thread per chunk (32 elements),
+// builds the 16-entry product table of the chunk's block in registers and
+// writes 64 B of output with 128-bit non-temporal stores.  Anything the fast
+// kernel cannot take (block size not a multiple of 32, unaligned pointers,
+// the last n % 32 elements) goes through the element-wise kernel, which
+// computes the same fp32 product and conversion.
+#include "abi_common.hpp"
+#include "nf4_device.hpp"
+
+namespace nf4s {
+
+__constant__ uint32_t kCodeTable[16] = {
+    0xbf800000u, 0xbf3239b1u, 0xbf066b30u, 0xbeca32a0u,
+    0xbe91a24du, 0xbe3d353fu, 0xbdba7872u, 0x00000000u,
+    0x3da2faffu, 0x3e24cae3u, 0x3e7c04ddu, 0x3ead033au,
+    0x3ee1a4b8u, 0x3f1007abu, 0x3f3913b3u, 0x3f800000u,
+};
+
+__device__ __forceinline__ float code_dyn(int i) {
+  return __builtin_bit_cast(float, kCodeTable[i]);
+}
+
+// ---------------------------------------------------------------------------
+// Quantize (shard_engine/python/pipeline/quantizer.py:21-53)
+// ---------------------------------------------------------------------------
+
+// NaN-propagating max, as torch's max(dim) over |x| (quantizer.py:35).
+__device__ __forceinline__ float max_nan(float a, float b) {
+  if (a != a) return a;
+  if (b != b) return b;
+  return b > a ? b : a;
+}
+
+// First-index argmin of |n - code_i| (quantizer.py:40-41) through the
+// bracketing pair: j = last code <= n, then j or j+1 by the same fp32
+// distances, j on ties.  Equal to the 16-way argmin for every fp32 n in
+// [-1, 1] (checked exhaustively against the literal form on the CPU).
+__device__ __forceinline__ uint32_t nf4_code(float n) {
+  int j = 0;
+#pragma unroll
+  for (int i = 1; i < 16; ++i) j += (n >= code_value(i)) ? 1 : 0;
+  if (n != n) return 0;  // torch argmin over an all-NaN row yields index 0
+  if (j == 15) return 15;
+  const float dl = fabsf(n - code_dyn(j));
+  const float dr = fabsf(n - code_dyn(j + 1));
+  return dr < dl ? (uint32_t)(j + 1) : (uint32_t)j;
+}
+
+// block_size == 64: one wave per block, one lane per element.
+__global__ void __launch_bounds__(256) quantize64_kernel(const float *__restrict__ x, int64_t n,
+                                                         uint8_t *__restrict__ packed,
+                                                         float *__restrict__ absmax,
+                                                         int64_t nblocks) {
+  const int lane = threadIdx.x & 63;
+  const int64_t wave0 = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int64_t nwaves = (int64_t)gridDim.x * (blockDim.x >> 6);
+  for (int64_t b = wave0; b < nblocks; b += nwaves) {
+    const int64_t e = b * 64 + lane;
+    const float v = (e < n) ? x[e] : 0.0f;  // zero padding, quantizer.py:30-32
+    float m = fabsf(v);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) m = max_nan(m, __shfl_xor(m, off, 64));
+    if (lane == 0) absmax[b] = m;                        // unclamped, :48-53
+    const float safe = (m < 1e-8f) ? 1e-8f : m;          // clamp(min=1e-8), :36
+    const float nv = v / safe;                           // correctly rounded, :38
+    uint32_t c = nf4_code(nv);
+    uint32_t c1 = __shfl_xor(c, 1, 64);
+    if (e + 1 >= n) c1 = 0;                              // odd-count pad nibble, :44-45
+    if ((lane & 1) == 0 && e < n) packed[e >> 1] = (uint8_t)((c << 4) | c1);  // :46
+  }
+}
+
+// Any block size: per-block absmax, then per-byte codes.
+__global__ void absmax_generic_kernel(const float *__restrict__ x, int64_t n, int32_t bs,
+                                      float *__restrict__ absmax, int64_t nblocks) {
+  for (int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; b < nblocks;
+       b += (int64_t)gridDim.x * blockDim.x) {
+    float m = 0.0f;
+    const int64_t s = b * bs;
+    for (int64_t i = s; i < s + bs && i < n; ++i) m = max_nan(m, fabsf(x[i]));
+    absmax[b] = m;
+  }
+}
+
+__global__ void codes_generic_kernel(const float *__restrict__ x, int64_t n, int32_t bs,
+                                     const float *__restrict__ absmax,
+                                     uint8_t *__restrict__ packed, int64_t npacked) {
+  for (int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j < npacked;
+       j += (int64_t)gridDim.x * blockDim.x) {
+    uint32_t byte = 0;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int64_t e = 2 * j + h;
+      uint32_t c = 0;
+      if (e < n) {
+        const float m = absmax[e / bs];
+        const float safe = (m < 1e-8f) ? 1e-8f : m;
+        c = nf4_code(x[e] / safe);
+      }
+      byte |= c << (h ? 0 : 4);
+    }
+    packed[j] = (uint8_t)byte;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Double-quant encode (conventions of galore/src/quantize.rs:4-13)
+// ---------------------------------------------------------------------------
+
+__global__ void __launch_bounds__(256) dq_encode_kernel(const float *__restrict__ absmax,
+                                                        int64_t nblocks, int32_t group,
+                                                        uint8_t *__restrict__ q,
+                                                        float *__restrict__ scale) {
+  __shared__ float red[4];
+  const int64_t g = blockIdx.x;
+  const int64_t s = g * group;
+  const int64_t e = (s + group < nblocks) ? s + group : nblocks;
+  float m = 0.0f;
+  for (int64_t i = s + threadIdx.x; i < e; i += blockDim.x) {
+    const float a = absmax[i];
+    m = (a > m) ? a : m;  // NaN never wins, as in the CPU encode
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float o = __shfl_xor(m, off, 64);
+    m = (o > m) ? o : m;
+  }
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  float mx = red[0];
+  for (int w = 1; w < (int)(blockDim.x >> 6); ++w) mx = (red[w] > mx) ? red[w] : mx;
+  const float sc = (mx <= 0.0f) ? 1.0f : mx / 127.0f;
+  if (threadIdx.x == 0) scale[g] = sc;
+  for (int64_t i = s + threadIdx.x; i < e; i += blockDim.x) {
+    float r = rintf(absmax[i] / sc);  // round half to even
+    if (!(r >= 0.0f)) r = 0.0f;
+    if (r > 127.0f) r = 127.0f;
+    q[i] = (uint8_t)r;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Dequant (shard_engine/src/nf4.rs:37-83)
+// ---------------------------------------------------------------------------
+
+constexpr int kMaxBatch = 16;
+constexpr int kDqThreads = 256;
+constexpr int kChunksPerThread = 4;  // 128 elements per thread per tile
+constexpr int64_t kTileChunks = (int64_t)kDqThreads * kChunksPerThread;
+
+struct DqEntry {
+  const uint8_t *packed;
+  AbsmaxRef am;
+  int32_t block_size;
+  uint16_t *out;
+  int64_t nchunks;     // full 32-element chunks handled here
+  int64_t tile_begin;  // first tile index of this entry in the launch
+};
+
+struct DqBatch {
+  DqEntry e[kMaxBatch];
+  int32_t count;
+};
+
+template <bool kF16>
+__global__ void __launch_bounds__(kDqThreads) dequant_fast_kernel(const DqBatch batch) {
+  // The workgroup's entry: tile ranges are uniform per workgroup.
+  const int64_t tile = blockIdx.x;
+  int idx = 0;
+#pragma unroll 1
+  for (int i = 1; i < batch.count; ++i)
+    if (tile >= batch.e[i].tile_begin) idx = i;
+  const DqEntry &E = batch.e[idx];
+  const int64_t c0 = (tile - E.tile_begin) * kTileChunks + threadIdx.x;
+  const u32x4 *src = reinterpret_cast<const u32x4 *>(E.packed);
+  u32x4 *dst = reinterpret_cast<u32x4 *>(E.out);
+
+  u32x4 w[kChunksPerThread];
+  float am[kChunksPerThread];
+#pragma unroll
+  for (int u = 0; u < kChunksPerThread; ++u) {
+    const int64_t c = c0 + (int64_t)u * kDqThreads;
+    if (c < E.nchunks) {
+      w[u] = __builtin_nontemporal_load(src + c);
+      am[u] = load_absmax(E.am, (c * 32) / E.block_size);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kChunksPerThread; ++u) {
+    const int64_t c = c0 + (int64_t)u * kDqThreads;
+    if (c < E.nchunks) {
+      const Lut16 lut = make_lut<kF16>(am[u]);
+      const uint32_t words[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        uint32_t o[4];
+        lut_apply8(lut, words[q], o);
+        u32x4 v;
+        v.x = o[0]; v.y = o[1]; v.z = o[2]; v.w = o[3];
+        __builtin_nontemporal_store(v, dst + c * 4 + q);
+      }
+    }
+  }
+}
+
+template <bool kF16>
+__global__ void dequant_elem_kernel(const uint8_t *__restrict__ packed, AbsmaxRef am,
+                                    int32_t bs, uint16_t *__restrict__ out, int64_t begin,
+                                    int64_t end) {
+  for (int64_t e = begin + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < end;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const uint32_t byte = packed[e >> 1];
+    const uint32_t nib = (e & 1) ? (byte & 15u) : (byte >> 4);
+    const float v = code_dyn((int)nib) * load_absmax(am, e / bs);
+    uint16_t r;
+    if (kF16) r = __builtin_bit_cast(uint16_t, (_Float16)v);
+    else r = __builtin_bit_cast(uint16_t, (__bf16)v);
+    out[e] = r;
+  }
+}
+
+static AbsmaxRef absmax_ref(const nf4s_tensor &t) {
+  AbsmaxRef a;
+  a.absmax = t.absmax;
+  a.q = t.absmax_q;
+  a.scale = t.absmax_scale;
+  a.group = t.dq_group > 0 ? t.dq_group : 1;
+  return a;
+}
+
+static bool fast_ok(const nf4s_tensor &t, const uint16_t *out) {
+  return t.block_size % 32 == 0 && aligned(t.packed, 16) && aligned(out, 16);
+}
+
+static int grid_for(int64_t work, int threads) {
+  int64_t g = (work + threads - 1) / threads;
+  if (g > 65536) g = 65536;
+  return (int)(g < 1 ? 1 : g);
+}
+
+template <bool kF16>
+static int32_t dequant_batch(const nf4s_tensor *ts, const int64_t *ns, uint16_t *const *outs,
+                             int32_t count, hipStream_t stream) {
+  if (count < 0 || count > kMaxBatch)
+    return fail(NF4S_ERR_INVALID_ARGUMENT, "batch count %d outside [0, %d]", count, kMaxBatch);
+  if (count > 0 && (ts == nullptr || ns == nullptr || outs == nullptr))
+    return fail(NF4S_ERR_INVALID_ARGUMENT, "batch arrays are NULL");
+  for (int i = 0; i < count; ++i) {
+    const int32_t rc = validate_tensor(&ts[i], ns[i]);
+    if (rc != NF4S_OK) return rc;
+    if (ns[i] > 0 && outs[i] == nullptr) return fail(NF4S_ERR_INVALID_ARGUMENT, "output is NULL");
+  }
+  DqBatch batch{};
+  int64_t tiles = 0;
+  for (int i = 0; i < count; ++i) {
+    const nf4s_tensor &t = ts[i];
+    const int64_t n = ns[i];
+    const bool fast = fast_ok(t, outs[i]);
+    const int64_t nchunks = fast ? n / 32 : 0;
+    if (nchunks > 0) {
+      DqEntry &E = batch.e[batch.count++];
+      E.packed = t.packed;
+      E.am = absmax_ref(t);
+      E.block_size = t.block_size;
+      E.out = outs[i];
+      E.nchunks = nchunks;
+      E.tile_begin = tiles;
+      tiles += (nchunks + kTileChunks - 1) / kTileChunks;
+    }
+    const int64_t tail_begin = nchunks * 32;
+    if (tail_begin < n) {
+      hipLaunchKernelGGL(dequant_elem_kernel<kF16>, dim3(grid_for(n - tail_begin, 256)),
+                         dim3(256), 0, stream, t.packed, absmax_ref(t), t.block_size, outs[i],
+                         tail_begin, n);
+      const int32_t rc = check_launch("dequant_elem_kernel");
+      if (rc != NF4S_OK) return rc;
+    }
+  }
+  if (tiles > 0) {
+    if (tiles > 0x7fffffff) return fail(NF4S_ERR_UNSUPPORTED_SHAPE, "too many tiles");
+    hipLaunchKernelGGL(dequant_fast_kernel<kF16>, dim3((uint32_t)tiles), dim3(kDqThreads), 0,
+                       stream, batch);
+    return check_launch("dequant_fast_kernel");
+  }
+  return NF4S_OK;
+}
+
+}  // namespace nf4s
+
+using namespace nf4s;
+
+extern "C" {
+
+int32_t nf4s_quantize(const float *x, int64_t n, int32_t block_size, uint8_t *packed,
+                      float *absmax, void *stream) {
+  if (n < 0) return fail(NF4S_ERR_INVALID_ARGUMENT, "negative element count");
+  if (block_size <= 0) return fail(NF4S_ERR_INVALID_ARGUMENT, "block_size must be positive");
+  if (n == 0) return NF4S_OK;
+  if (x == nullptr || packed == nullptr || absmax == nullptr)
+    return fail(NF4S_ERR_INVALID_ARGUMENT, "NULL buffer");
+  const int64_t nb = (n + block_size - 1) / block_size;
+  hipStream_t s = as_stream(stream);
+  if (block_size == 64) {
+    const int64_t wg = (nb + 3) / 4;
+    hipLaunchKernelGGL(quantize64_kernel, dim3(grid_for(wg, 1)), dim3(256), 0, s, x, n, packed,
+                       absmax, nb);
+    return check_launch("quantize64_kernel");
+  }
+  hipLaunchKernelGGL(absmax_generic_kernel, dim3(grid_for(nb, 256)), dim3(256), 0, s, x, n,
+                     block_size, absmax, nb);
+  int32_t rc = check_launch("absmax_generic_kernel");
+  if (rc != NF4S_OK) return rc;
+  const int64_t npk = (n + 1) / 2;
+  hipLaunchKernelGGL(codes_generic_kernel, dim3(grid_for(npk, 256)), dim3(256), 0, s, x, n,
+                     block_size, absmax, packed, npk);
+  return check_launch("codes_generic_kernel");
+}
+
+int32_t nf4s_dq_encode(const float *absmax, int64_t nblocks, int32_t group, uint8_t *q,
+                       float *scale, void *stream) {
+  if (nblocks < 0 || group <= 0)
+    return fail(NF4S_ERR_INVALID_ARGUMENT, "nblocks must be >= 0 and group > 0");
+  if (nblocks == 0) return NF4S_OK;
+  if (absmax == nullptr || q == nullptr || scale == nullptr)
+    return fail(NF4S_ERR_INVALID_ARGUMENT, "NULL buffer");
+  const int64_t ng = (nblocks + group - 1) / group;
+  if (ng > 0x7fffffff) return fail(NF4S_ERR_UNSUPPORTED_SHAPE, "too many groups");
+  hipLaunchKernelGGL(dq_encode_kernel, dim3((uint32_t)ng), dim3(256), 0, as_stream(stream),
+                     absmax, nblocks, group, q, scale);
+  return check_launch("dq_encode_kernel");
+}
+
+int32_t nf4s_dequant_f16(const nf4s_tensor *t, int64_t n, uint16_t *out, void *stream) {
+  if (t == nullptr) return fail(NF4S_ERR_INVALID_ARGUMENT, "tensor descriptor is NULL");
+  uint16_t *outs[1] = {out};
+  return dequant_batch<true>(t, &n, outs, 1, as_stream(stream));
+}
+
+int32_t nf4s_dequant_bf16(const nf4s_tensor *t, int64_t n, uint16_t *out, void *stream) {
+  if (t == nullptr) return fail(NF4S_ERR_INVALID_ARGUMENT, "tensor descriptor is NULL");
+  uint16_t *outs[1] = {out};
+  return dequant_batch<false>(t, &n, outs, 1, as_stream(stream));
+}
+
+int32_t nf4s_dequant_batch_bf16(const nf4s_tensor *ts, const int64_t *ns, uint16_t *const *outs,
+                                int32_t count, void *stream) {
+  return dequant_batch<false>(ts, ns, outs, count, as_stream(stream));
+}
+
+}  // extern "C"

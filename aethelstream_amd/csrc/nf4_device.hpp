@@ -1,0 +1,126 @@
+// nf4_device.hpp - device-side NF4 helpers shared by the codec and GEMM
+// kernels (gfx950).
+//
+// The hot dequant step turns one 32-bit word of packed nibbles (8 elements)
+// into four bf16x2 (or f16x2) words with a per-block product table held in
+// registers and looked up with v_perm_b32 byte selects:
+//   T[i] = cvt(code[i] * absmax)          16 products, one fp32 multiply each
+// so every output is bit-identical to cvt(code * absmax) computed per element
+// (shard_engine/src/nf4.rs:76-78): each product depends on (code, absmax) only.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace nf4s {
+
+// Native clang vector types (usable with the nontemporal builtins).
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// shard_engine/src/nf4.rs:6-23, as fp32 bit patterns.
+__device__ constexpr uint32_t kCodeBits[16] = {
+    0xbf800000u, 0xbf3239b1u, 0xbf066b30u, 0xbeca32a0u,
+    0xbe91a24du, 0xbe3d353fu, 0xbdba7872u, 0x00000000u,
+    0x3da2faffu, 0x3e24cae3u, 0x3e7c04ddu, 0x3ead033au,
+    0x3ee1a4b8u, 0x3f1007abu, 0x3f3913b3u, 0x3f800000u,
+};
+
+__device__ __forceinline__ float code_value(int i) {
+  return __builtin_bit_cast(float, kCodeBits[i]);
+}
+
+// fp32 -> bf16 bits, round to nearest even (v_cvt_pk_bf16_f32 on gfx950).
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  const __bf16 a = (__bf16)lo;
+  const __bf16 b = (__bf16)hi;
+  return (uint32_t)__builtin_bit_cast(uint16_t, a) |
+         ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+}
+
+// fp32 -> IEEE binary16 bits, round to nearest even (v_cvt_f16_f32).
+__device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
+  const _Float16 a = (_Float16)lo;
+  const _Float16 b = (_Float16)hi;
+  return (uint32_t)__builtin_bit_cast(uint16_t, a) |
+         ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+}
+
+__device__ __forceinline__ uint32_t perm(uint32_t hi4, uint32_t lo4, uint32_t sel) {
+  // Result byte i = byte sel.byte[i] of the 8-byte value {hi4:lo4}.
+  return __builtin_amdgcn_perm(hi4, lo4, sel);
+}
+
+// Byte-split product table: lo[t] holds the low bytes of entries 4t..4t+3,
+// hi[t] their high bytes.
+struct Lut16 {
+  uint32_t lo[4];
+  uint32_t hi[4];
+};
+
+template <bool kF16>
+__device__ __forceinline__ Lut16 make_lut(float absmax) {
+  uint32_t d[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float p0 = code_value(2 * j) * absmax;
+    const float p1 = code_value(2 * j + 1) * absmax;
+    d[j] = kF16 ? pack_f16x2(p0, p1) : pack_bf16x2(p0, p1);
+  }
+  Lut16 t;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    // d[2q] = {T[4q], T[4q+1]}, d[2q+1] = {T[4q+2], T[4q+3]}.
+    t.lo[q] = perm(d[2 * q + 1], d[2 * q], 0x06040200u);
+    t.hi[q] = perm(d[2 * q + 1], d[2 * q], 0x07050301u);
+  }
+  return t;
+}
+
+// 16-entry byte lookup: 3-bit index in each selector byte, bit 3 of the
+// nibble given as a per-byte 0x00/0xff mask.
+__device__ __forceinline__ uint32_t lookup16(const uint32_t tab[4], uint32_t sel,
+                                             uint32_t mask) {
+  const uint32_t a = perm(tab[1], tab[0], sel);  // entries 0..7
+  const uint32_t b = perm(tab[3], tab[2], sel);  // entries 8..15
+  return (b & mask) | (a & ~mask);
+}
+
+// Dequantize the 8 elements of one packed word w (byte k holds element 2k in
+// its high nibble and 2k+1 in its low nibble).  out[j] = elem 2j | elem 2j+1
+// << 16, i.e. natural element order in memory.
+__device__ __forceinline__ void lut_apply8(const Lut16 &t, uint32_t w, uint32_t out[4]) {
+  const uint32_t selE = (w >> 4) & 0x07070707u;
+  const uint32_t selO = w & 0x07070707u;
+  const uint32_t mE = w & 0x80808080u;
+  const uint32_t maskE = (mE << 1) - (mE >> 7);
+  const uint32_t mO = w & 0x08080808u;
+  const uint32_t maskO = (mO << 5) - (mO >> 3);
+  const uint32_t loE = lookup16(t.lo, selE, maskE);
+  const uint32_t hiE = lookup16(t.hi, selE, maskE);
+  const uint32_t loO = lookup16(t.lo, selO, maskO);
+  const uint32_t hiO = lookup16(t.hi, selO, maskO);
+  const uint32_t e01 = perm(hiE, loE, 0x05010400u);  // elem0, elem2
+  const uint32_t e23 = perm(hiE, loE, 0x07030602u);  // elem4, elem6
+  const uint32_t o01 = perm(hiO, loO, 0x05010400u);  // elem1, elem3
+  const uint32_t o23 = perm(hiO, loO, 0x07030602u);  // elem5, elem7
+  out[0] = perm(o01, e01, 0x05040100u);
+  out[1] = perm(o01, e01, 0x07060302u);
+  out[2] = perm(o23, e23, 0x05040100u);
+  out[3] = perm(o23, e23, 0x07060302u);
+}
+
+// Per-block absmax, fp32 or double-quantized: (float)q * scale[b / group].
+struct AbsmaxRef {
+  const float *absmax;
+  const uint8_t *q;
+  const float *scale;
+  int32_t group;
+};
+
+__device__ __forceinline__ float load_absmax(const AbsmaxRef &a, int64_t blk) {
+  if (a.q == nullptr) return a.absmax[blk];
+  return (float)a.q[blk] * a.scale[blk / a.group];
+}
+
+}  // namespace nf4s

@@ -1,0 +1,78 @@
+"""The C-ABI library loads and exports every symbol include/nf4stream.h declares;
+argument validation mirrors the reference's error rules.  CPU only: the calls
+below are rejected before any kernel launch."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from aethelstream_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "nf4stream.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(nf4s_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_symbols_exported():
+    lib = _lib.load()
+    syms = declared_symbols()
+    assert len(syms) >= 10
+    for s in syms:
+        assert hasattr(lib, s), f"libnf4stream.so does not export {s}"
+    # The ctypes table covers the header exactly.
+    assert sorted(_lib.SIGNATURES) == syms
+
+
+def test_abi_version_and_strerror():
+    lib = _lib.load()
+    assert lib.nf4s_abi_version() == 1
+    assert lib.nf4s_strerror(0) == b"ok"
+    assert b"nf4_absmax" in lib.nf4s_strerror(_lib.NF4S_ERR_ABSMAX_TOO_SMALL)
+    assert b"nf4_packed" in lib.nf4s_strerror(_lib.NF4S_ERR_PACKED_TOO_SMALL)
+
+
+def _desc(packed_len, absmax_len, bs, dq=False, scale_len=0, group=0):
+    # Non-null dummy pointers: validation must reject before dereferencing.
+    fake = 0x1000
+    return _lib.Nf4sTensor(packed=fake, packed_len=packed_len,
+                           absmax=None if dq else fake, absmax_q=fake if dq else None,
+                           absmax_scale=fake if dq else None, absmax_len=absmax_len,
+                           scale_len=scale_len, block_size=bs, dq_group=group)
+
+
+def test_malformed_absmax_then_packed():
+    # shard_engine/src/nf4.rs:46-57: absmax first, then packed; same text.
+    lib = _lib.load()
+    d = _desc(packed_len=8, absmax_len=1, bs=8)
+    rc = lib.nf4s_dequant_f16(ctypes.byref(d), 16, 0x2000, None)
+    assert rc == _lib.NF4S_ERR_ABSMAX_TOO_SMALL
+    assert lib.nf4s_last_error_message() == b"absmax too small: 1 < 2"
+    d = _desc(packed_len=3, absmax_len=4, bs=2)
+    rc = lib.nf4s_dequant_bf16(ctypes.byref(d), 8, 0x2000, None)
+    assert rc == _lib.NF4S_ERR_PACKED_TOO_SMALL
+    assert lib.nf4s_last_error_message() == b"packed too small: 6 < 8"
+
+
+def test_invalid_arguments():
+    lib = _lib.load()
+    assert lib.nf4s_dequant_bf16(None, 8, 0x2000, None) == _lib.NF4S_ERR_INVALID_ARGUMENT
+    d = _desc(packed_len=4, absmax_len=1, bs=0)
+    assert lib.nf4s_dequant_bf16(ctypes.byref(d), 8, 0x2000, None) == _lib.NF4S_ERR_INVALID_ARGUMENT
+    d = _desc(packed_len=4, absmax_len=1, bs=64, dq=True, scale_len=0, group=256)
+    assert lib.nf4s_dequant_bf16(ctypes.byref(d), 8, 0x2000, None) == _lib.NF4S_ERR_ABSMAX_TOO_SMALL
+    assert lib.nf4s_quantize(None, 10, 64, None, None, None) == _lib.NF4S_ERR_INVALID_ARGUMENT
+    assert lib.nf4s_quantize(0x1000, 10, 0, 0x1000, 0x1000, None) == _lib.NF4S_ERR_INVALID_ARGUMENT
+    assert lib.nf4s_dq_encode(0x1000, 10, 0, 0x1000, 0x1000, None) == _lib.NF4S_ERR_INVALID_ARGUMENT
+
+
+def test_python_mirror_raises_malformed_index():
+    import torch
+    from aethelstream_amd import nf4
+    with pytest.raises(ValueError):
+        nf4.dequant_nf4_into(torch.zeros(4, dtype=torch.uint8), torch.ones(1),
+                             torch.zeros(8, dtype=torch.float16), 64)

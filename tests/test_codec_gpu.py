@@ -1,0 +1,215 @@
+"""GPU parity of the NF4 codec kernels (quantize, double-quant, dequant)
+against the CPU oracle: bit-exact codes, absmax, double-quant codes/scales and
+f16/bf16 dequant outputs."""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from aethelstream_amd import nf4
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+GOLDEN = np.load(os.path.join(os.path.dirname(__file__), "golden", "nf4_golden.npz"))
+CASES = sorted({k.split("__")[0] for k in GOLDEN.files})
+
+
+def _bits16(t: torch.Tensor) -> np.ndarray:
+    return t.view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def _dev(a: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def _gpu_dequant(packed, absmax, n, bs, f16, q=None, scale=None, group=0,
+                 packed_off=0, out_off=0):
+    """Dequant through the C ABI, optionally from/to deliberately unaligned views."""
+    pk = torch.zeros(packed.size + packed_off, dtype=torch.uint8, device=DEV)
+    pk[packed_off:] = _dev(packed)
+    w = nf4.Nf4Weight(packed=pk[packed_off:], absmax=None if q is not None else _dev(absmax),
+                      shape=[n], block_size=bs,
+                      absmax_q=None if q is None else _dev(q),
+                      absmax_scale=None if q is None else _dev(scale),
+                      dq_group=group)
+    dt = torch.float16 if f16 else torch.bfloat16
+    buf = torch.full((n + out_off,), float("nan"), dtype=dt, device=DEV)
+    nf4.dequant(w, out=buf[out_off:])
+    torch.cuda.synchronize()
+    return _bits16(buf[out_off:])
+
+
+def test_kats_on_device():
+    # shard_engine/src/nf4.rs:118-143.
+    out = _gpu_dequant(np.array([0x7F], np.uint8), np.array([1.0], np.float32), 2, 2, True)
+    assert out.tolist() == [0x0000, 0x3C00]
+    out = _gpu_dequant(np.array([0x7F, 0x70], np.uint8), np.array([1.0, 1.0], np.float32),
+                       3, 2, True)
+    assert out.tolist() == [0x0000, 0x3C00, 0x0000]
+    # dequant_nf4_alloc: n = 2 * len(packed).
+    r = nf4.dequant_nf4_alloc(_dev(np.array([0x7F], np.uint8)), _dev(np.array([1.0], np.float32)), 2)
+    assert _bits16(r).tolist() == [0x0000, 0x3C00]
+
+
+def test_malformed_index_on_device():
+    with pytest.raises(nf4.MalformedIndex, match="nf4_absmax"):
+        nf4.dequant_nf4_into(_dev(np.zeros(8, np.uint8)), _dev(np.ones(1, np.float32)),
+                             torch.empty(16, dtype=torch.float16, device=DEV), 8)
+    with pytest.raises(nf4.MalformedIndex, match="packed too small: 6 < 8"):
+        nf4.dequant_nf4_into(_dev(np.zeros(3, np.uint8)), _dev(np.ones(4, np.float32)),
+                             torch.empty(8, dtype=torch.float16, device=DEV), 2)
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_golden_fixtures(case):
+    x = GOLDEN[f"{case}__x"]
+    r = nf4.quantize_nf4(_dev(x))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(r.packed.cpu().numpy(), GOLDEN[f"{case}__packed"])
+    np.testing.assert_array_equal(r.absmax.cpu().numpy().view(np.uint32),
+                                  GOLDEN[f"{case}__absmax"].view(np.uint32))
+    n = x.size
+    p, a = GOLDEN[f"{case}__packed"], GOLDEN[f"{case}__absmax"]
+    np.testing.assert_array_equal(_gpu_dequant(p, a, n, 64, True), GOLDEN[f"{case}__f16"])
+    np.testing.assert_array_equal(_gpu_dequant(p, a, n, 64, False), GOLDEN[f"{case}__bf16"])
+
+
+@pytest.mark.parametrize("n", [1, 2, 31, 32, 33, 63, 64, 65, 1000, 4096 + 17, 65536, 300001])
+@pytest.mark.parametrize("bs", [2, 32, 64, 100, 128])
+def test_quantize_and_dequant_vs_oracle(n, bs):
+    x = oracle.gen_normal(1000 + n + bs, n, 0.02)
+    pk_ref, am_ref = oracle.quantize_nf4(x, bs)
+    r = nf4.quantize_nf4(_dev(x), block_size=bs)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(r.packed.cpu().numpy(), pk_ref)
+    np.testing.assert_array_equal(r.absmax.cpu().numpy().view(np.uint32), am_ref.view(np.uint32))
+    for f16 in (True, False):
+        ref = (oracle.dequant_f16 if f16 else oracle.dequant_bf16)(pk_ref, am_ref, n, bs)
+        np.testing.assert_array_equal(_gpu_dequant(pk_ref, am_ref, n, bs, f16), ref)
+
+
+@pytest.mark.parametrize("packed_off,out_off", [(1, 0), (0, 1), (3, 5), (16, 8)])
+def test_unaligned_buffers(packed_off, out_off):
+    n = 8192 + 96
+    x = oracle.gen_normal(77, n, 0.02)
+    pk, am = oracle.quantize_nf4(x)
+    ref = oracle.dequant_bf16(pk, am, n)
+    got = _gpu_dequant(pk, am, n, 64, False, packed_off=packed_off, out_off=out_off)
+    np.testing.assert_array_equal(got, ref)
+
+
+def test_extreme_absmax_subnormal_and_overflow():
+    # Products that are fp32 subnormals (bf16 keeps them; f16 flushes by RNE),
+    # and f16 overflow to inf (half's from_f32 semantics).
+    rng = np.random.default_rng(5)
+    n = 64 * 64
+    pk = rng.integers(0, 256, n // 2, dtype=np.uint8)
+    am = np.concatenate([np.full(16, 3e-39, np.float32), np.full(16, 1e-42, np.float32),
+                         np.full(16, 70000.0, np.float32), np.full(16, 6e-5, np.float32)])
+    for f16 in (True, False):
+        ref = (oracle.dequant_f16 if f16 else oracle.dequant_bf16)(pk, am, n)
+        np.testing.assert_array_equal(_gpu_dequant(pk, am, n, 64, f16), ref)
+
+
+def test_double_quant_encode_and_dequant():
+    n = 64 * 256 * 5 + 64 * 77          # a partial last group
+    x = oracle.gen_normal(99, n, 0.02)
+    pk, am = oracle.quantize_nf4(x)
+    q_ref, s_ref = oracle.dq_encode(am, 256)
+    q, s = nf4.dq_encode(_dev(am), 256)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(q.cpu().numpy(), q_ref)
+    np.testing.assert_array_equal(s.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
+    am2 = oracle.dq_decode(q_ref, s_ref, 256)
+    for f16 in (True, False):
+        ref = (oracle.dequant_f16 if f16 else oracle.dequant_bf16)(pk, am2, n)
+        got = _gpu_dequant(pk, None, n, 64, f16, q=q_ref, scale=s_ref, group=256)
+        np.testing.assert_array_equal(got, ref)
+
+
+def test_dq_encode_zero_group():
+    am = np.abs(oracle.gen_normal(3, 1024, 0.05))
+    am[256:512] = 0
+    q, s = nf4.dq_encode(_dev(am), 256)
+    q_ref, s_ref = oracle.dq_encode(am, 256)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(q.cpu().numpy(), q_ref)
+    np.testing.assert_array_equal(s.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
+
+
+def test_config1_4096x4096_bitexact():
+    # fp32 4096x4096 ~ N(0, 0.02), block 64, fp32 absmax.
+    n = 4096 * 4096
+    x = oracle.gen_normal(42, n, 0.02)
+    pk_ref, am_ref = oracle.quantize_nf4(x)
+    w = nf4.quantize_weight(_dev(x).view(4096, 4096))
+    out = nf4.dequant(w)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(w.packed.cpu().numpy(), pk_ref)
+    np.testing.assert_array_equal(w.absmax.cpu().numpy().view(np.uint32), am_ref.view(np.uint32))
+    np.testing.assert_array_equal(_bits16(out).reshape(-1), oracle.dequant_bf16(pk_ref, am_ref, n))
+    out16 = nf4.dequant(w, dtype=torch.float16)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(_bits16(out16).reshape(-1), oracle.dequant_f16(pk_ref, am_ref, n))
+
+
+LAYER_7B = [("q", 4096, 4096), ("k", 4096, 4096), ("v", 4096, 4096), ("o", 4096, 4096),
+            ("gate", 11008, 4096), ("up", 11008, 4096), ("down", 4096, 11008)]
+
+
+def test_config2_7b_layer_batch_dequant_dq():
+    # the 7 matrices of a Llama-7B layer, double-quant, one
+    # grouped launch; every output element compared with the oracle.
+    g = torch.Generator(device=DEV).manual_seed(2)
+    ws = []
+    for i, (_, r, c) in enumerate(LAYER_7B):
+        wf = torch.randn(r, c, device=DEV, generator=g) * 0.02
+        w = nf4.quantize_weight(wf, double_quant=True)
+        # Codes of the first and last 64 rows against the oracle quantizer.
+        for rows in (slice(0, 64), slice(r - 64, r)):
+            xs = wf[rows].contiguous().cpu().numpy()
+            pk_ref, am_ref = oracle.quantize_nf4(xs)
+            start = rows.start * c // 2
+            np.testing.assert_array_equal(
+                w.packed[start:start + pk_ref.size].cpu().numpy(), pk_ref)
+        del wf
+        ws.append(w)
+    outs = nf4.dequant_batch(ws)
+    torch.cuda.synchronize()
+    for w, o in zip(ws, outs):
+        am2 = oracle.dq_decode(w.absmax_q.cpu().numpy(), w.absmax_scale.cpu().numpy(), 256)
+        ref = oracle.dequant_bf16(w.packed.cpu().numpy(), am2, w.numel)
+        np.testing.assert_array_equal(_bits16(o).reshape(-1), ref)
+
+
+def test_batch_mixed_and_empty():
+    xs = [oracle.gen_normal(s, n, 0.02) for s, n in ((1, 64 * 100), (2, 1000), (3, 64 * 7 + 33))]
+    ws, refs = [], []
+    for i, x in enumerate(xs):
+        pk, am = oracle.quantize_nf4(x)
+        if i == 1:
+            q, s = oracle.dq_encode(am, 256)
+            ws.append(nf4.Nf4Weight(packed=_dev(pk), absmax=None, shape=[x.size], absmax_q=_dev(q),
+                                    absmax_scale=_dev(s), dq_group=256))
+            am = oracle.dq_decode(q, s, 256)
+        else:
+            ws.append(nf4.Nf4Weight(packed=_dev(pk), absmax=_dev(am), shape=[x.size]))
+        refs.append(oracle.dequant_bf16(pk, am, x.size))
+    outs = nf4.dequant_batch(ws)
+    torch.cuda.synchronize()
+    for o, r in zip(outs, refs):
+        np.testing.assert_array_equal(_bits16(o), r)
+    assert nf4.dequant_batch([]) == []
+
+
+def test_quantizer_mirror_fidelity():
+    # quantizer.py:77-81 through the device mirror (weight-scale data).
+    x = (torch.randn(256, 256, device=DEV) * 0.02).half()
+    r = nf4.quantize_nf4(x)
+    ok, mse = nf4.check_fidelity(x, r)
+    assert ok and mse < 1e-5
+    assert r.original_shape == [256, 256]
+    z = nf4.quantize_nf4(torch.zeros(64, 64, device=DEV, dtype=torch.float16))
+    assert nf4.dequantize_nf4(z).abs().max().item() < 1e-5

@@ -1,0 +1,190 @@
+"""Pins the CPU oracle (oracle/nf4_oracle.c) against the reference's own known
+answers, the torch restatement fixtures and the mathematics.  CPU only."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+
+GOLDEN = np.load(__import__("os").path.join(__import__("os").path.dirname(__file__),
+                                            "golden", "nf4_golden.npz"))
+CASES = sorted({k.split("__")[0] for k in GOLDEN.files})
+
+# shard_engine/src/nf4.rs:6-23 as bits (the survey's table of the literals).
+CODE_BITS = [0xbf800000, 0xbf3239b1, 0xbf066b30, 0xbeca32a0, 0xbe91a24d, 0xbe3d353f,
+             0xbdba7872, 0x00000000, 0x3da2faff, 0x3e24cae3, 0x3e7c04dd, 0x3ead033a,
+             0x3ee1a4b8, 0x3f1007ab, 0x3f3913b3, 0x3f800000]
+
+
+def test_codebook_bits_and_zero_at_index_7():
+    cb = oracle.codebook()
+    assert cb.view(np.uint32).tolist() == CODE_BITS
+    assert cb[7] == 0.0                               # nf4.rs:113-116
+    assert np.all(np.diff(cb) > 0)
+    # quantizer.py:5-10 builds the table from Python doubles: same fp32 bits.
+    lits = [-1.0, -0.6961928, -0.52507305, -0.3949175, -0.28444138, -0.18477343,
+            -0.09105004, 0.0, 0.0795803, 0.1609302, 0.2461123, 0.33791524,
+            0.44070983, 0.562617, 0.72295684, 1.0]
+    assert np.array(lits).astype(np.float32).view(np.uint32).tolist() == CODE_BITS
+    # flowcast's incompatible table differs at index 6; this one must not.
+    assert CODE_BITS[6] != 0xbdba7871
+
+
+def test_kat_roundtrip_accuracy():
+    # nf4.rs:118-130: 0x7F -> [0.0, 1.0] with absmax 1, block 2.
+    out = oracle.dequant_f16(np.array([0x7F], np.uint8), np.array([1.0], np.float32), 2, 2)
+    assert out.tolist() == [0x0000, 0x3C00]
+
+
+def test_kat_partial_block():
+    # nf4.rs:132-143: [0x7F, 0x70], block 2, 3 elements -> [0, 1, 0].
+    out = oracle.dequant_f16(np.array([0x7F, 0x70], np.uint8),
+                             np.array([1.0, 1.0], np.float32), 3, 2)
+    assert out.tolist() == [0x0000, 0x3C00, 0x0000]
+
+
+def test_malformed_index_rules():
+    # nf4.rs:46-57: absmax checked first, then packed.
+    with pytest.raises(ValueError, match="absmax too small"):
+        oracle.dequant_f16(np.zeros(8, np.uint8), np.ones(1, np.float32), 16, 8)
+    with pytest.raises(ValueError, match="packed too small"):
+        oracle.dequant_f16(np.zeros(3, np.uint8), np.ones(4, np.float32), 8, 2)
+    # dequant_nf4_alloc (nf4.rs:98-107): n = 2 * len(packed).
+    out = oracle.dequant_f16(np.array([0x0F, 0x80], np.uint8), np.array([2.0], np.float32), 4, 64)
+    assert [oracle.lib().or_f32_to_f16(v) for v in (-2.0, 2.0, 0.0795803 * 2, -2.0)] == \
+        [int(v) for v in out]
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_quantize_matches_torch_restatement(case):
+    x = GOLDEN[f"{case}__x"]
+    packed, absmax = oracle.quantize_nf4(x)
+    np.testing.assert_array_equal(packed, GOLDEN[f"{case}__packed"])
+    np.testing.assert_array_equal(absmax.view(np.uint32), GOLDEN[f"{case}__absmax"].view(np.uint32))
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_dequant_matches_torch_conversion(case):
+    n = GOLDEN[f"{case}__x"].size
+    p, a = GOLDEN[f"{case}__packed"], GOLDEN[f"{case}__absmax"]
+    np.testing.assert_array_equal(oracle.dequant_f16(p, a, n), GOLDEN[f"{case}__f16"])
+    np.testing.assert_array_equal(oracle.dequant_bf16(p, a, n), GOLDEN[f"{case}__bf16"])
+
+
+def test_bracket_rule_exhaustive():
+    # Every fp32 in [-1, 1]: the two-candidate rule equals the 16-way argmin.
+    assert oracle.lib().or_check_bracket_exhaustive(0) == 0
+
+
+def test_argmin_first_index_on_exact_tie():
+    # A planted tie: n exactly halfway (in fp32 distance) must take the lower code.
+    cb = oracle.codebook()
+    found = 0
+    for i in range(15):
+        m = np.float32((np.float64(cb[i]) + np.float64(cb[i + 1])) / 2)
+        for cand in (m, np.nextafter(m, np.float32(-2)), np.nextafter(m, np.float32(2))):
+            dl, dr = abs(cand - cb[i]), abs(cand - cb[i + 1])
+            if dl == dr:
+                found += 1
+                assert oracle.lib().or_nf4_code_argmin(float(cand)) == i
+                assert oracle.lib().or_nf4_code_bracket(float(cand)) == i
+    assert found > 0
+
+
+def test_quantize_special_cases():
+    # Zero block -> absmax 0, every code 7 (0.0); test_nf4_fidelity.py:14-20.
+    p, a = oracle.quantize_nf4(np.zeros(128, np.float32))
+    assert np.all(a == 0) and np.all(p == 0x77)
+    # +-absmax -> codes 15 / 0.
+    x = np.zeros(64, np.float32)
+    x[0], x[1] = 0.5, -0.5
+    p, a = oracle.quantize_nf4(x)
+    assert a[0] == np.float32(0.5) and p[0] == 0xF0
+    # Sizes: ceil(n/2) bytes, ceil(n/64) blocks (test_nf4_fidelity.py:29-43).
+    for n in (128, 200, 201, 1):
+        p, a = oracle.quantize_nf4(np.ones(n, np.float32))
+        assert p.size == (n + 1) // 2 and a.size == (n + 63) // 64
+    # Odd count: pad nibble is code 0.
+    p, _ = oracle.quantize_nf4(np.ones(3, np.float32))
+    assert p[1] & 0x0F == 0
+
+
+def test_quantize_mse_bound():
+    # test_nf4_fidelity.py:5-12 asks MSE <= 1e-3 for fp16 randn(256,256).  With
+    # this algorithm (64-element blocks, 16 codes) the MSE of unit-variance data
+    # is ~8.5e-3 * sigma^2, so that reference test cannot pass at sigma = 1; the
+    # bound holds at weight scale (sigma = 0.02, the configs' weights).
+    g = torch.Generator().manual_seed(42)
+    x = torch.randn(256, 256, generator=g).half().float().numpy()
+    p, a = oracle.quantize_nf4(x)
+    y = oracle.dequant_f16(p, a, x.size).view(np.float16).astype(np.float32)
+    rel = float(np.mean((x.reshape(-1) - y) ** 2))
+    assert 0.005 < rel < 0.012
+    w = (torch.randn(256, 256, generator=g) * 0.02).half().float().numpy()
+    p, a = oracle.quantize_nf4(w)
+    y = oracle.dequant_f16(p, a, w.size).view(np.float16).astype(np.float32)
+    assert float(np.mean((w.reshape(-1) - y) ** 2)) <= 1e-3
+
+
+def test_f16_rne_against_numpy():
+    rng = np.random.default_rng(0)
+    bits = rng.integers(0, 2 ** 32, 200000, dtype=np.uint64).astype(np.uint32)
+    x = bits.view(np.float32)
+    x = x[np.isfinite(x)]
+    special = np.array([65504, 65519.99, 65520, 6.1035156e-05, 5.9604645e-08, 2.9802322e-08,
+                        2.9802326e-08, 1e-45, 0.0, -0.0, 1.0000001, 2049.0, 2051.0],
+                       np.float32)
+    x = np.concatenate([x, special, -special])
+    ours = np.array([oracle.lib().or_f32_to_f16(float(v)) for v in x], np.uint16)
+    with np.errstate(over="ignore"):
+        ref = x.astype(np.float16).view(np.uint16)
+    np.testing.assert_array_equal(ours, ref)
+
+
+def test_bf16_rne_against_torch():
+    rng = np.random.default_rng(1)
+    bits = rng.integers(0, 2 ** 32, 200000, dtype=np.uint64).astype(np.uint32)
+    x = bits.view(np.float32)
+    x = x[np.isfinite(x)]
+    ours = np.array([oracle.lib().or_f32_to_bf16(float(v)) for v in x[:20000]], np.uint16)
+    ref = torch.from_numpy(x[:20000].copy()).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    np.testing.assert_array_equal(ours, ref)
+    np.testing.assert_array_equal(oracle.f32_to_bf16_bits(x), torch.from_numpy(x.copy()).to(
+        torch.bfloat16).view(torch.int16).numpy().view(np.uint16))
+
+
+def test_dq_invariants():
+    a = np.abs(oracle.gen_normal(7, 1000, 0.05)).astype(np.float32)
+    a[256:512] = 0.0                                 # an all-zero group
+    q, s = oracle.dq_encode(a, 256)
+    assert s.size == 4 and q.max() <= 127
+    assert s[1] == 1.0 and np.all(q[256:512] == 0)
+    for g in range(4):
+        blk = a[g * 256:(g + 1) * 256]
+        if blk.max() > 0:
+            assert s[g] == np.float32(blk.max() / np.float32(127))
+            assert q[g * 256 + int(np.argmax(blk))] == 127
+    dec = oracle.dq_decode(q, s, 256)
+    assert np.all(np.abs(dec - a) <= s[np.arange(a.size) // 256] * 0.5 * (1 + 1e-6))
+
+
+def test_matmul_tb_and_dgrad_against_fp64():
+    rng = np.random.default_rng(3)
+    a = rng.standard_normal((5, 37)).astype(np.float32)
+    b = rng.standard_normal((11, 37)).astype(np.float32)
+    c = oracle.matmul_tb(a, b)
+    np.testing.assert_allclose(c, a.astype(np.float64) @ b.T.astype(np.float64), rtol=1e-5, atol=1e-5)
+    dy = rng.standard_normal((5, 11)).astype(np.float32)
+    dx = oracle.dgrad(dy, b)
+    np.testing.assert_allclose(dx, dy.astype(np.float64) @ b.astype(np.float64), rtol=1e-5, atol=1e-5)
+    # dx accumulates into the caller's buffer (backward.rs:157 zero-inits it).
+    acc = np.ones((5, 37), np.float32)
+    oracle.lib().or_dgrad(oracle._p(dy), oracle._p(b), 5, 11, 37, oracle._p(acc))
+    np.testing.assert_allclose(acc, dx + 1, rtol=1e-5, atol=1e-5)
+
+
+def test_generator_statistics():
+    x = oracle.gen_normal(42, 1 << 18, 0.02)
+    assert abs(float(x.mean())) < 2e-4
+    assert abs(float(x.std()) - 0.02) < 2e-4
+    assert np.array_equal(x, oracle.gen_normal(42, 1 << 18, 0.02))
