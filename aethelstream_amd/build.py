@@ -26,6 +26,8 @@ HIP_FLAGS = [
     "-fPIC",
     "-Wall",
     "-Wno-unused-function",
+    # Every fp32 operation rounds on its own, as in the reference.
+    "-ffp-contract=off",
     # Packed fp32 VALU ops stay off: plain scalar fp32 code only.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]

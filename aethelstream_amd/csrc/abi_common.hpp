@@ -26,6 +26,13 @@ inline bool aligned(const void *p, uintptr_t a) {
   return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0;
 }
 
+// log2 of a power-of-two double-quant group (validate_tensor checks it).
+inline int32_t group_shift(int32_t group) {
+  int32_t s = 0;
+  while ((1 << s) < group) ++s;
+  return s;
+}
+
 // Validates `t` for reading n elements: the two MalformedIndex checks of
 // shard_engine/src/nf4.rs:46-57 (same order, same message text), plus the
 // pointer and double-quant fields.

@@ -40,8 +40,9 @@ int32_t validate_tensor(const nf4s_tensor *t, int64_t n) {
   if (n > 0 && t->packed == nullptr)
     return fail(NF4S_ERR_INVALID_ARGUMENT, "packed is NULL");
   if (dq) {
-    if (t->dq_group <= 0)
-      return fail(NF4S_ERR_INVALID_ARGUMENT, "dq_group must be positive, got %d", t->dq_group);
+    if (t->dq_group <= 0 || (t->dq_group & (t->dq_group - 1)) != 0)
+      return fail(NF4S_ERR_INVALID_ARGUMENT, "dq_group must be a power of two, got %d",
+                  t->dq_group);
     const int64_t ng = (nb + t->dq_group - 1) / t->dq_group;
     if (t->scale_len < ng || (ng > 0 && t->absmax_scale == nullptr))
       return fail(NF4S_ERR_ABSMAX_TOO_SMALL, "absmax scale too small: %lld < %lld",

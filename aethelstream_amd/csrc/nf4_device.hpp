@@ -30,20 +30,28 @@ __device__ __forceinline__ float code_value(int i) {
   return __builtin_bit_cast(float, kCodeBits[i]);
 }
 
-// fp32 -> bf16 bits, round to nearest even (v_cvt_pk_bf16_f32 on gfx950).
-__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  const __bf16 a = (__bf16)lo;
-  const __bf16 b = (__bf16)hi;
-  return (uint32_t)__builtin_bit_cast(uint16_t, a) |
-         ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+// The reference rounds twice: the fp32 product code * absmax, then the f16 /
+// bf16 conversion (shard_engine/src/nf4.rs:77-78).  hipcc otherwise folds
+// fptrunc(fmul) into one v_fma_mix* with a single rounding of the exact
+// product (even under -ffp-contract=off), which differs on conversion ties.
+// The empty asm hands the conversion an opaque, already-rounded fp32 value.
+__device__ __forceinline__ float fp32_rounded(float x) {
+  asm("" : "+v"(x));
+  return x;
 }
 
-// fp32 -> IEEE binary16 bits, round to nearest even (v_cvt_f16_f32).
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
+// fp32 pair -> bf16 pair, round to nearest even: one v_cvt_pk_bf16_f32.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo, hi}, bf16x2_t));
+}
+
+// fp32 pair -> IEEE binary16 pair, round to nearest even: one v_cvt_pk_f16_f32.
 __device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
-  const _Float16 a = (_Float16)lo;
-  const _Float16 b = (_Float16)hi;
-  return (uint32_t)__builtin_bit_cast(uint16_t, a) |
-         ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo, hi}, f16x2_t));
 }
 
 __device__ __forceinline__ uint32_t perm(uint32_t hi4, uint32_t lo4, uint32_t sel) {
@@ -63,8 +71,8 @@ __device__ __forceinline__ Lut16 make_lut(float absmax) {
   uint32_t d[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    const float p0 = code_value(2 * j) * absmax;
-    const float p1 = code_value(2 * j + 1) * absmax;
+    const float p0 = fp32_rounded(code_value(2 * j) * absmax);
+    const float p1 = fp32_rounded(code_value(2 * j + 1) * absmax);
     d[j] = kF16 ? pack_f16x2(p0, p1) : pack_bf16x2(p0, p1);
   }
   Lut16 t;
@@ -110,17 +118,18 @@ __device__ __forceinline__ void lut_apply8(const Lut16 &t, uint32_t w, uint32_t 
   out[3] = perm(o23, e23, 0x07060302u);
 }
 
-// Per-block absmax, fp32 or double-quantized: (float)q * scale[b / group].
+// Per-block absmax, fp32 or double-quantized: (float)q * scale[b >> shift]
+// (groups of 2^shift blocks).
 struct AbsmaxRef {
   const float *absmax;
   const uint8_t *q;
   const float *scale;
-  int32_t group;
+  int32_t group_shift;
 };
 
 __device__ __forceinline__ float load_absmax(const AbsmaxRef &a, int64_t blk) {
   if (a.q == nullptr) return a.absmax[blk];
-  return (float)a.q[blk] * a.scale[blk / a.group];
+  return (float)a.q[blk] * a.scale[blk >> a.group_shift];
 }
 
 }  // namespace nf4s

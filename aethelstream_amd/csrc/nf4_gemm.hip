@@ -1,0 +1,416 @@
+// nf4_gemm.hip - NF4-dequant-fused bf16 GEMM for gfx950 (MI355X).
+//
+//   forward  y[m,n]  = x[m,k]  . W^T   (matmul_tb, doublepass/src/math.rs:9-21)
+//   dgrad    dx[m,k] = dy[m,n] . W     (doublepass/src/backward.rs:79-85, ...)
+// with W [n,k] NF4 (blocks of 64 along k, fp32 or double-quantized absmax),
+// bf16 activations, fp32 accumulation in v_mfma_f32_32x32x16_bf16, bf16 out.
+//
+// Workgroup = 4 waves, tile = 512 rows of the activation x 128 output columns.
+// Each wave owns 128 rows and keeps a 128x128 fp32 accumulator (16 MFMA
+// tiles of 32x32, 256 registers).  Per 64-deep reduction step:
+//   * each wave loads its activation fragments straight from global memory
+//     into registers (no LDS round trip, no sharing needed: rows are private
+//     to the wave); the next step's fragments are in flight during this one;
+//   * the workgroup dequantizes the step's 128x64 weight tile ONCE into LDS
+//     as bf16 (16-entry per-block product table in registers, v_perm_b32
+//     lookups), so the dequant cost is amortised over 512 activation rows;
+//   * all 4 waves read the weight fragments from LDS and issue 64 MFMAs.
+// The weight tile of step t+1 is dequantized while step t's MFMAs run (two
+// LDS buffers, one workgroup barrier per step).
+//
+// MFMA operand layout used (32x32x16): lane l supplies row / column l % 32
+// and 8 reduction slots from lane group g = l / 32.  The kernel assigns
+// reduction index 32g + 8s + e to slot e of sub-step s for BOTH operands, so
+// a lane's 4 sub-steps read 64 contiguous bytes of its activation row.  The
+// accumulator layout is lane l: column l % 32, row 8(v/4) + 4g + v%4.
+#include "abi_common.hpp"
+#include "nf4_device.hpp"
+
+namespace nf4s {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+constexpr int kGemmThreads = 256;
+constexpr int kTileM = 512;   // activation rows per workgroup (128 per wave)
+constexpr int kTileO = 128;   // output columns per workgroup
+constexpr int kStep = 64;     // reduction depth per step (= NF4 block size)
+
+struct GemmArgs {
+  const uint16_t *a;  // activation [M, R] row-major (x or dy)
+  int64_t lda;
+  uint16_t *out;      // [M, O] row-major (y or dx)
+  int64_t ldo;
+  int64_t M, O, R;    // rows, output columns, reduction length
+  const uint8_t *packed;
+  AbsmaxRef am;
+  int64_t wk;         // columns of W (its k); W row stride = wk/2 bytes
+  int64_t wn;         // rows of W (its n)
+  int32_t tiles_m, tiles_o;
+};
+
+// LDS tile: 128 rows x 64 bf16 (128 B = 8 units of 16 B).  Unit u of row r
+// lives at r*8 + (u ^ (r & 7)) so that the 32 rows a wave reads for one
+// fragment spread over all banks.
+__device__ __forceinline__ int lds_unit(int row, int u) { return row * 8 + (u ^ (row & 7)); }
+
+// Absmax of block `blk`: fp32, or the double-quant code times its group scale.
+// A template flag rather than a runtime test keeps the GEMM step one basic
+// block (one scheduling region).
+template <bool kDQ>
+__device__ __forceinline__ float absmax_at(const AbsmaxRef &a, int64_t blk) {
+  if (kDQ) return (float)a.q[blk] * a.scale[blk >> a.group_shift];
+  return a.absmax[blk];
+}
+
+// Forward producer: thread -> (row n_local = tid/2, half h = tid%2), 32
+// consecutive k of one block; writes 4 swizzled 16-B units of its row.
+template <bool kDQ>
+struct FwdProducer {
+  static constexpr int kDsWritesPerWord = 1;
+  const uint8_t *ptr;   // packed bytes of (row, half) at step 0
+  int64_t am_idx;       // absmax block index at step 0
+  int row, h;
+  __device__ void init(const GemmArgs &g, int64_t o0) {
+    row = threadIdx.x >> 1;
+    h = threadIdx.x & 1;
+    int64_t n = o0 + row;
+    if (n >= g.wn) n = g.wn - 1;  // ragged N: clamp (outputs are not stored)
+    ptr = g.packed + n * (g.wk >> 1) + 16 * h;
+    am_idx = n * (g.wk >> 6);
+  }
+  __device__ __forceinline__ void load(const GemmArgs &g, int64_t step, u32x4 &w, float &a) const {
+    w = *reinterpret_cast<const u32x4 *>(ptr + step * 32);
+    a = absmax_at<kDQ>(g.am, am_idx + step);
+  }
+  __device__ __forceinline__ Lut16 table(float a) const { return make_lut<false>(a); }
+  // Dequantizes packed word k (8 elements) into LDS.
+  __device__ __forceinline__ void put(u32x4 *lds, const Lut16 &lut, uint32_t word, int k) const {
+    uint32_t o[4];
+    lut_apply8(lut, word, o);
+    u32x4 v;
+    v.x = o[0]; v.y = o[1]; v.z = o[2]; v.w = o[3];
+    lds[lds_unit(row, 4 * h + k)] = v;
+  }
+  __device__ __forceinline__ void store(u32x4 *lds, const u32x4 &w, float a) const {
+    const Lut16 lut = table(a);
+    put(lds, lut, w.x, 0);
+    put(lds, lut, w.y, 1);
+    put(lds, lut, w.z, 2);
+    put(lds, lut, w.w, 3);
+  }
+};
+
+// Dgrad producer: the step covers W rows n0..n0+63 (the reduction) and W
+// columns o0..o0+127 (the output).  Thread -> (W row r = tid/4, quarter
+// q = tid%4): 32 consecutive columns of one block.  The LDS tile is stored
+// transposed (LDS row = output column, 64 reduction values per row), so
+// each element is written as one 16-bit value.
+template <bool kDQ>
+struct DgradProducer {
+  static constexpr int kDsWritesPerWord = 8;
+  const uint8_t *ptr;
+  int64_t am_idx;
+  int r, q;
+  uint32_t valid_mask;  // all ones when the thread's columns exist
+  __device__ void init(const GemmArgs &g, int64_t o0) {
+    r = threadIdx.x >> 2;
+    q = threadIdx.x & 3;
+    const int64_t col = o0 + 32 * q;
+    const bool valid = col < g.wk;
+    valid_mask = valid ? 0xffffffffu : 0u;
+    const int64_t c = valid ? col : 0;
+    ptr = g.packed + (int64_t)r * (g.wk >> 1) + (c >> 1);
+    am_idx = (int64_t)r * (g.wk >> 6) + (c >> 6);
+  }
+  __device__ __forceinline__ void load(const GemmArgs &g, int64_t step, u32x4 &w, float &a) const {
+    // Step s covers W rows 64s .. 64s+63.
+    w = *reinterpret_cast<const u32x4 *>(ptr + step * 64 * (g.wk >> 1));
+    a = absmax_at<kDQ>(g.am, am_idx + step * 64 * (g.wk >> 6));
+  }
+  __device__ __forceinline__ Lut16 table(float a) const {
+    // Columns beyond k read column 0's bytes and are zeroed via the absmax.
+    return make_lut<false>(__builtin_bit_cast(float, __builtin_bit_cast(uint32_t, a) & valid_mask));
+  }
+  __device__ __forceinline__ void put(u32x4 *lds, const Lut16 &lut, uint32_t word, int k) const {
+    uint32_t o[4];
+    lut_apply8(lut, word, o);
+    uint16_t *l16 = reinterpret_cast<uint16_t *>(lds);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int col = 32 * q + 8 * k + j;  // LDS row (output column)
+      const uint16_t v = (uint16_t)((j & 1) ? (o[j >> 1] >> 16) : (o[j >> 1] & 0xffffu));
+      l16[lds_unit(col, r >> 3) * 8 + (r & 7)] = v;
+    }
+  }
+  __device__ __forceinline__ void store(u32x4 *lds, const u32x4 &w, float a) const {
+    const Lut16 lut = table(a);
+    put(lds, lut, w.x, 0);
+    put(lds, lut, w.y, 1);
+    put(lds, lut, w.z, 2);
+    put(lds, lut, w.w, 3);
+  }
+};
+
+// Maps the workgroup index to (tile_m, tile_o).  Workgroups are dispatched
+// round-robin over the 8 XCDs; consecutive logical tiles (same activation
+// rows, neighbouring output columns) are given to the same XCD so that its
+// resident workgroups share the activation rows in that XCD's L2.
+__device__ __forceinline__ void map_tile(int tiles_m, int tiles_o, int &tm, int &to) {
+  const int T = tiles_m * tiles_o;
+  const int b = blockIdx.x;
+  const int x = b & 7, qq = b >> 3;
+  const int base = T >> 3, rem = T & 7;
+  const int L = x * base + (x < rem ? x : rem) + qq;
+  tm = L / tiles_o;
+  to = L - tm * tiles_o;
+}
+
+// sched_group_barrier masks
+constexpr int kSgMfma = 0x008, kSgValu = 0x002, kSgVmemRead = 0x020;
+constexpr int kSgDsRead = 0x100, kSgDsWrite = 0x200;
+
+// One 64-deep reduction step.  Reads the weight tile from LDS buffer B and
+// accumulates 64 MFMAs in 4 sub-steps of 16.  Alongside, it
+//   * loads the weight bytes of step t+2 (wn_, an_),
+//   * dequantizes step t+1's weights (wc, ac) into LDS buffer Bn, one packed
+//     word (8 elements) per sub-step, the product table in sub-step 0,
+//   * refills each sub-step's activation fragments with the next step's once
+//     that sub-step's MFMAs have read them (one register set).
+// Each sub-step is its own scheduling region (sched_barrier fences) in which
+// sched_group_barrier spreads the VALU, LDS and global-memory instructions
+// between the MFMAs: a wave issues in order, so VALU work only overlaps the
+// matrix pipe when it sits between MFMAs in the instruction stream.
+template <class Producer>
+__device__ __forceinline__ void gemm_step(const GemmArgs &g, const Producer &prod,
+                                          floatx16 (&acc)[4][4], u32x4 (&A)[4][4],
+                                          const u32x4 &wc, float ac, u32x4 &wn_, float &an_,
+                                          const uint16_t *const (&arow)[4], const u32x4 *B,
+                                          u32x4 *Bn, int64_t t, int64_t nsteps, int jl,
+                                          int grp) {
+  const int64_t t1 = (t + 1 < nsteps) ? t + 1 : nsteps - 1;
+  const int64_t t2 = (t + 2 < nsteps) ? t + 2 : nsteps - 1;
+  prod.load(g, t2, wn_, an_);
+  const uint32_t words[4] = {wc.x, wc.y, wc.z, wc.w};
+  Lut16 lut;
+  u32x4 b[2][4];
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt) b[0][nt] = B[lds_unit(32 * nt + jl, 4 * grp)];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    if (s == 0) lut = prod.table(ac);
+    if (s < 3) {
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt)
+        b[(s + 1) & 1][nt] = B[lds_unit(32 * nt + jl, 4 * grp + s + 1)];
+    }
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt)
+        acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+            __builtin_bit_cast(bf16x8, A[mt][s]), __builtin_bit_cast(bf16x8, b[s & 1][nt]),
+            acc[mt][nt], 0, 0, 0);
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+      A[mt][s] = *reinterpret_cast<const u32x4 *>(arow[mt] + t1 * kStep + 8 * s);
+    prod.put(Bn, lut, words[s], s);
+
+    // 16 MFMAs: VALU (table + one word ~28-60 ops), 4 fragment reads for
+    // the next sub-step early, the 4 activation refills late (they must
+    // follow the MFMAs that read those registers), LDS writes at the end.
+    if (s == 0) __builtin_amdgcn_sched_group_barrier(kSgVmemRead, 2, 0);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      __builtin_amdgcn_sched_group_barrier(kSgMfma, 1, 0);
+      if (s == 0) __builtin_amdgcn_sched_group_barrier(kSgValu, 4, 0);
+      else __builtin_amdgcn_sched_group_barrier(kSgValu, 2, 0);
+      if (s < 3 && i < 4) __builtin_amdgcn_sched_group_barrier(kSgDsRead, 1, 0);
+      if (i >= 12) __builtin_amdgcn_sched_group_barrier(kSgVmemRead, 1, 0);
+      if (i >= 8 && i < 8 + Producer::kDsWritesPerWord)
+        __builtin_amdgcn_sched_group_barrier(kSgDsWrite, 1, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+template <class Producer>
+__global__ void __launch_bounds__(kGemmThreads, 1) nf4_gemm_kernel(const GemmArgs g) {
+  __shared__ u32x4 lds[2][128 * 8];
+
+  int tm, to;
+  map_tile(g.tiles_m, g.tiles_o, tm, to);
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int jl = lane & 31;
+  const int grp = lane >> 5;
+  const int64_t m0 = (int64_t)tm * kTileM + wave * 128;
+  const int64_t o0 = (int64_t)to * kTileO;
+  const int64_t nsteps = g.R / kStep;
+
+  // Activation fragment pointers: row m0 + 32*mt + jl (clamped), columns
+  // 32*grp + 8*s + (0..7) of each step.
+  const uint16_t *arow[4];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) {
+    int64_t r = m0 + 32 * mt + jl;
+    if (r >= g.M) r = g.M - 1;
+    arow[mt] = g.a + r * g.lda + 32 * grp;
+  }
+
+  Producer prod;
+  prod.init(g, o0);
+
+  floatx16 acc[4][4];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[mt][nt][v] = 0.0f;
+
+  u32x4 A[4][4];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      A[mt][s] = *reinterpret_cast<const u32x4 *>(arow[mt] + 8 * s);
+  {
+    u32x4 w0;
+    float a0;
+    prod.load(g, 0, w0, a0);
+    prod.store(lds[0], w0, a0);
+  }
+  // wc/ac: weights of step t+1 (dequantized during step t); wn/an: step t+2.
+  u32x4 wc, wn;
+  float ac, an;
+  prod.load(g, nsteps > 1 ? 1 : 0, wc, ac);
+  __syncthreads();
+
+  // One loop body for every step.  The last step's "next" work reads clamped
+  // (valid) addresses and writes the LDS buffer nobody reads again.
+#pragma unroll 1
+  for (int64_t t = 0; t < nsteps; ++t) {
+    const int buf = (int)(t & 1);
+    gemm_step<Producer>(g, prod, acc, A, wc, ac, wn, an, arow, lds[buf], lds[buf ^ 1], t, nsteps,
+                        jl, grp);
+    __syncthreads();
+    wc = wn;
+    ac = an;
+  }
+
+  // Epilogue: fp32 -> bf16 (RNE), lane l writes column o0 + 32nt + l%32.
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+      const int64_t col = o0 + 32 * nt + jl;
+      if (col >= g.O) continue;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int64_t row = m0 + 32 * mt + 8 * (v >> 2) + 4 * grp + (v & 3);
+        if (row < g.M) {
+          const __bf16 h = (__bf16)acc[mt][nt][v];
+          g.out[row * g.ldo + col] = __builtin_bit_cast(uint16_t, h);
+        }
+      }
+    }
+}
+
+static AbsmaxRef absmax_of(const nf4s_tensor &t) {
+  AbsmaxRef a;
+  a.absmax = t.absmax;
+  a.q = t.absmax_q;
+  a.scale = t.absmax_scale;
+  a.group_shift = t.dq_group > 0 ? group_shift(t.dq_group) : 0;
+  return a;
+}
+
+// Shared argument checks of the two GEMM entry points.  W is [wn, wk].
+static int32_t check_gemm(const uint16_t *act, const nf4s_tensor *w, int64_t m, int64_t wn,
+                          int64_t wk, const uint16_t *out) {
+  if (act == nullptr || out == nullptr)
+    return fail(NF4S_ERR_INVALID_ARGUMENT, "activation or output is NULL");
+  if (m < 0 || wn <= 0 || wk <= 0)
+    return fail(NF4S_ERR_INVALID_ARGUMENT, "bad GEMM shape m=%lld n=%lld k=%lld",
+                (long long)m, (long long)wn, (long long)wk);
+  const int32_t rc = validate_tensor(w, wn * wk);
+  if (rc != NF4S_OK) return rc;
+  if (w->block_size != 64)
+    return fail(NF4S_ERR_UNSUPPORTED_SHAPE, "fused GEMM needs block_size 64, got %d",
+                w->block_size);
+  if (wk % 64 != 0)
+    return fail(NF4S_ERR_UNSUPPORTED_SHAPE, "fused GEMM needs k %% 64 == 0, got %lld",
+                (long long)wk);
+  if (!aligned(act, 16) || !aligned(w->packed, 16))
+    return fail(NF4S_ERR_MISALIGNED, "activation and packed weights must be 16-byte aligned");
+  if (!aligned(out, 2)) return fail(NF4S_ERR_MISALIGNED, "output must be 2-byte aligned");
+  return NF4S_OK;
+}
+
+template <class Producer>
+static int32_t launch_gemm(const GemmArgs &g, hipStream_t s, const char *name) {
+  const int64_t T = (int64_t)g.tiles_m * g.tiles_o;
+  if (T == 0) return NF4S_OK;
+  if (T > 0x7fffffff) return fail(NF4S_ERR_UNSUPPORTED_SHAPE, "too many tiles");
+  hipLaunchKernelGGL(nf4_gemm_kernel<Producer>, dim3((uint32_t)T), dim3(kGemmThreads), 0, s, g);
+  return check_launch(name);
+}
+
+}  // namespace nf4s
+
+using namespace nf4s;
+
+extern "C" {
+
+int32_t nf4s_gemm_fwd(const uint16_t *x, const nf4s_tensor *w, int64_t m, int64_t n, int64_t k,
+                      uint16_t *y, void *stream) {
+  int32_t rc = check_gemm(x, w, m, n, k, y);
+  if (rc != NF4S_OK) return rc;
+  if (m == 0) return NF4S_OK;
+  GemmArgs g{};
+  g.a = x;
+  g.lda = k;
+  g.out = y;
+  g.ldo = n;
+  g.M = m;
+  g.O = n;
+  g.R = k;
+  g.packed = w->packed;
+  g.am = absmax_of(*w);
+  g.wk = k;
+  g.wn = n;
+  g.tiles_m = (int32_t)((m + kTileM - 1) / kTileM);
+  g.tiles_o = (int32_t)((n + kTileO - 1) / kTileO);
+  if (w->absmax_q != nullptr)
+    return launch_gemm<FwdProducer<true>>(g, as_stream(stream), "nf4_gemm_fwd");
+  return launch_gemm<FwdProducer<false>>(g, as_stream(stream), "nf4_gemm_fwd");
+}
+
+int32_t nf4s_gemm_dgrad(const uint16_t *dy, const nf4s_tensor *w, int64_t m, int64_t n,
+                        int64_t k, uint16_t *dx, void *stream) {
+  int32_t rc = check_gemm(dy, w, m, n, k, dx);
+  if (rc != NF4S_OK) return rc;
+  if (n % 64 != 0)
+    return fail(NF4S_ERR_UNSUPPORTED_SHAPE, "dgrad needs n %% 64 == 0, got %lld", (long long)n);
+  if (m == 0) return NF4S_OK;
+  GemmArgs g{};
+  g.a = dy;
+  g.lda = n;
+  g.out = dx;
+  g.ldo = k;
+  g.M = m;
+  g.O = k;
+  g.R = n;
+  g.packed = w->packed;
+  g.am = absmax_of(*w);
+  g.wk = k;
+  g.wn = n;
+  g.tiles_m = (int32_t)((m + kTileM - 1) / kTileM);
+  g.tiles_o = (int32_t)((k + kTileO - 1) / kTileO);
+  if (w->absmax_q != nullptr)
+    return launch_gemm<DgradProducer<true>>(g, as_stream(stream), "nf4_gemm_dgrad");
+  return launch_gemm<DgradProducer<false>>(g, as_stream(stream), "nf4_gemm_dgrad");
+}
+
+}  // extern "C"

@@ -53,7 +53,7 @@ typedef struct nf4s_tensor {
     int64_t absmax_len;         /* entries in absmax / absmax_q */
     int64_t scale_len;          /* entries in absmax_scale (0 without dq) */
     int32_t block_size;         /* elements per block (64 in the reference) */
-    int32_t dq_group;           /* blocks per scale (256), 0 without dq */
+    int32_t dq_group;           /* blocks per scale, a power of two (256); 0 without dq */
 } nf4s_tensor;
 
 /* NF4S_ABI_VERSION of the loaded library. */

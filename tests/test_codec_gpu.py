@@ -213,3 +213,45 @@ def test_quantizer_mirror_fidelity():
     assert r.original_shape == [256, 256]
     z = nf4.quantize_nf4(torch.zeros(64, 64, device=DEV, dtype=torch.float16))
     assert nf4.dequantize_nf4(z).abs().max().item() < 1e-5
+
+
+def _tie_absmax(kind: str, count: int, seed: int = 0) -> np.ndarray:
+    """absmax values a for which fl32(code_i * a) lands exactly on an f16 (or
+    bf16) rounding midpoint while the exact product does not: a single-rounding
+    fused multiply-convert gives a different answer from the reference's
+    fp32-product-then-RNE there."""
+    cb = oracle.codebook().astype(np.float64)
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < count:
+        i = int(rng.integers(0, 16))
+        if cb[i] in (0.0, 1.0, -1.0):
+            continue
+        if kind == "f16":
+            h = np.float16(rng.uniform(0.01, 1.0))
+            mid = (float(h) + float(np.nextafter(h, np.float16(2)))) / 2
+        else:
+            b = np.float32(rng.uniform(0.01, 1.0)).view(np.uint32) & 0xFFFF0000
+            mid = float(np.uint32(b | 0x8000).view(np.float32))
+        a0 = np.float32(abs(mid / cb[i]))
+        for a in (a0, np.nextafter(a0, np.float32(0)), np.nextafter(a0, np.float32(9))):
+            p = np.float32(np.float32(cb[i]) * a)
+            if float(p) == abs(mid) * np.sign(cb[i]) and float(cb[i]) * float(a) != float(p):
+                out.append((i, a))
+                break
+    return out
+
+
+@pytest.mark.parametrize("bs", [64, 2])
+@pytest.mark.parametrize("kind", ["f16", "bf16"])
+def test_double_rounding_ties(kind, bs):
+    # Regression: the conversion must round the fp32 product, not the exact one.
+    ties = _tie_absmax(kind, 256 if bs == 64 else 2048, seed=bs)
+    nb = len(ties)
+    n = nb * bs
+    am = np.array([a for _, a in ties], np.float32)
+    codes = np.array([[i] * bs for i, _ in ties], np.uint8).reshape(-1)
+    pk = ((codes[0::2] << 4) | codes[1::2]).astype(np.uint8)
+    f16 = kind == "f16"
+    ref = (oracle.dequant_f16 if f16 else oracle.dequant_bf16)(pk, am, n, bs)
+    np.testing.assert_array_equal(_gpu_dequant(pk, am, n, bs, f16), ref)
