@@ -167,66 +167,87 @@ __device__ __forceinline__ void map_tile(int tiles_m, int tiles_o, int &tm, int 
 }
 
 // sched_group_barrier masks
-constexpr int kSgMfma = 0x008, kSgValu = 0x002, kSgVmemRead = 0x020;
+constexpr int kSgMfma = 0x008, kSgValu = 0x002, kSgVmem = 0x010;
 constexpr int kSgDsRead = 0x100, kSgDsWrite = 0x200;
 
-// One 64-deep reduction step.  Reads the weight tile from LDS buffer B and
-// accumulates 64 MFMAs in 4 sub-steps of 16.  Alongside, it
-//   * loads the weight bytes of step t+2 (wn_, an_),
-//   * dequantizes step t+1's weights (wc, ac) into LDS buffer Bn, one packed
-//     word (8 elements) per sub-step, the product table in sub-step 0,
-//   * refills each sub-step's activation fragments with the next step's once
-//     that sub-step's MFMAs have read them (one register set).
+// LDS: two activation buffers (per wave 128 rows x 128 B = 16 KB; 4 waves =
+// 64 KB each) and two weight tiles (16 KB each): 160 KB, the gfx950 maximum.
+__shared__ u32x4 g_lds_a0[4 * 1024];
+__shared__ u32x4 g_lds_a1[4 * 1024];
+__shared__ u32x4 g_lds_b0[1024];
+__shared__ u32x4 g_lds_b1[1024];
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// One 64-deep reduction step.  The activation tile of this step is in
+// LDS (this wave's part of Acur), the weight tile in Bcur.  Alongside the 64
+// MFMAs it
+//   * starts the direct-to-LDS loads of the next step's activation tile into
+//     Anext (16 instructions of 1 KB, 8 full 128-B rows each),
+//   * loads the packed weight bytes of step t+2 (wn_, an_),
+//   * dequantizes step t+1's weights (wc, ac) into Bnext, one packed word
+//     (8 elements) per sub-step, the product table in sub-step 0.
 // Each sub-step is its own scheduling region (sched_barrier fences) in which
-// sched_group_barrier spreads the VALU, LDS and global-memory instructions
-// between the MFMAs: a wave issues in order, so VALU work only overlaps the
-// matrix pipe when it sits between MFMAs in the instruction stream.
+// sched_group_barrier places VALU, LDS and memory instructions between the
+// MFMAs: a wave issues in order, so other work only overlaps the matrix pipe
+// when it sits between MFMAs in the instruction stream.
 template <class Producer>
 __device__ __forceinline__ void gemm_step(const GemmArgs &g, const Producer &prod,
-                                          floatx16 (&acc)[4][4], u32x4 (&A)[4][4],
+                                          floatx16 (&acc)[4][4], const u32x4 *__restrict__ Acur,
+                                          u32x4 *__restrict__ Anext_wave,
+                                          const u32x4 *__restrict__ Bcur,
+                                          u32x4 *__restrict__ Bnext,
+                                          const char *abase, const uint32_t (&aoff)[16],
                                           const u32x4 &wc, float ac, u32x4 &wn_, float &an_,
-                                          const uint16_t *const (&arow)[4], const u32x4 *B,
-                                          u32x4 *Bn, int64_t t, int64_t nsteps, int jl,
-                                          int grp) {
+                                          int64_t t, int64_t nsteps, int jl, int grp) {
   const int64_t t1 = (t + 1 < nsteps) ? t + 1 : nsteps - 1;
   const int64_t t2 = (t + 2 < nsteps) ? t + 2 : nsteps - 1;
-  prod.load(g, t2, wn_, an_);
   const uint32_t words[4] = {wc.x, wc.y, wc.z, wc.w};
   Lut16 lut;
-  u32x4 b[2][4];
+  // Fragments of sub-step s: A (4 m-tiles) and B (4 n-tiles), double-buffered.
+  u32x4 a[2][4], b[2][4];
 #pragma unroll
-  for (int nt = 0; nt < 4; ++nt) b[0][nt] = B[lds_unit(32 * nt + jl, 4 * grp)];
+  for (int i = 0; i < 4; ++i) {
+    const int row = 32 * i + jl;
+    a[0][i] = Acur[lds_unit(row, grp)];
+    b[0][i] = Bcur[lds_unit(row, grp)];
+  }
+  prod.load(g, t2, wn_, an_);
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
     if (s == 0) lut = prod.table(ac);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const char *src = abase + t1 * (kStep * 2) + aoff[4 * s + i];
+      __builtin_amdgcn_global_load_lds(src, (lds_void_t *)(Anext_wave + (4 * s + i) * 64), 16, 0,
+                                       0);
+    }
     if (s < 3) {
 #pragma unroll
-      for (int nt = 0; nt < 4; ++nt)
-        b[(s + 1) & 1][nt] = B[lds_unit(32 * nt + jl, 4 * grp + s + 1)];
+      for (int i = 0; i < 4; ++i) {
+        const int row = 32 * i + jl;
+        a[(s + 1) & 1][i] = Acur[lds_unit(row, 2 * (s + 1) + grp)];
+        b[(s + 1) & 1][i] = Bcur[lds_unit(row, 2 * (s + 1) + grp)];
+      }
     }
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
       for (int nt = 0; nt < 4; ++nt)
         acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-            __builtin_bit_cast(bf16x8, A[mt][s]), __builtin_bit_cast(bf16x8, b[s & 1][nt]),
+            __builtin_bit_cast(bf16x8, a[s & 1][mt]), __builtin_bit_cast(bf16x8, b[s & 1][nt]),
             acc[mt][nt], 0, 0, 0);
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
-      A[mt][s] = *reinterpret_cast<const u32x4 *>(arow[mt] + t1 * kStep + 8 * s);
-    prod.put(Bn, lut, words[s], s);
+    prod.put(Bnext, lut, words[s], s);
 
-    // 16 MFMAs: VALU (table + one word ~28-60 ops), 4 fragment reads for
-    // the next sub-step early, the 4 activation refills late (they must
-    // follow the MFMAs that read those registers), LDS writes at the end.
-    if (s == 0) __builtin_amdgcn_sched_group_barrier(kSgVmemRead, 2, 0);
+    // 16 MFMAs; the dequant's VALU (table + one word, ~28-60 ops) 4 per MFMA;
+    // the next sub-step's 8 fragment reads early; 4 DMA loads; LDS writes late.
+    if (s == 0) __builtin_amdgcn_sched_group_barrier(kSgVmem, 2, 0);
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       __builtin_amdgcn_sched_group_barrier(kSgMfma, 1, 0);
-      if (s == 0) __builtin_amdgcn_sched_group_barrier(kSgValu, 4, 0);
-      else __builtin_amdgcn_sched_group_barrier(kSgValu, 2, 0);
-      if (s < 3 && i < 4) __builtin_amdgcn_sched_group_barrier(kSgDsRead, 1, 0);
-      if (i >= 12) __builtin_amdgcn_sched_group_barrier(kSgVmemRead, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSgValu, 4, 0);
+      if (s < 3 && i < 8) __builtin_amdgcn_sched_group_barrier(kSgDsRead, 1, 0);
+      if (i >= 2 && i < 6) __builtin_amdgcn_sched_group_barrier(kSgVmem, 1, 0);
       if (i >= 8 && i < 8 + Producer::kDsWritesPerWord)
         __builtin_amdgcn_sched_group_barrier(kSgDsWrite, 1, 0);
     }
@@ -236,11 +257,9 @@ __device__ __forceinline__ void gemm_step(const GemmArgs &g, const Producer &pro
 
 template <class Producer>
 __global__ void __launch_bounds__(kGemmThreads, 1) nf4_gemm_kernel(const GemmArgs g) {
-  __shared__ u32x4 lds[2][128 * 8];
-
   int tm, to;
   map_tile(g.tiles_m, g.tiles_o, tm, to);
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int jl = lane & 31;
   const int grp = lane >> 5;
@@ -248,14 +267,26 @@ __global__ void __launch_bounds__(kGemmThreads, 1) nf4_gemm_kernel(const GemmArg
   const int64_t o0 = (int64_t)to * kTileO;
   const int64_t nsteps = g.R / kStep;
 
-  // Activation fragment pointers: row m0 + 32*mt + jl (clamped), columns
-  // 32*grp + 8*s + (0..7) of each step.
-  const uint16_t *arow[4];
+  // Direct-to-LDS activation loads: instruction i writes rows 8i..8i+7 of the
+  // wave's 128-row tile as 1 KB, lane p at LDS unit 64i + p, i.e. row
+  // 8i + p/8, physical unit p%8, which holds logical unit (p%8) ^ (row%8)
+  // (the swizzle of lds_unit).  aoff[i] is lane p's byte offset from the
+  // wave's first (clamped) row at k = 0; rows beyond M are clamped.
+  const int64_t mb = (m0 < g.M) ? m0 : g.M - 1;
+  const char *abase = reinterpret_cast<const char *>(g.a + mb * g.lda);
+  // Rows available to this wave from mb (at least 1, at most 128).
+  const int64_t avail64 = g.M - mb;
+  const int32_t avail = (int32_t)(avail64 > 128 ? 128 : avail64);
+  const uint32_t lda2 = (uint32_t)(g.lda * 2);
+  const int32_t skip = (int32_t)(m0 - mb);  // > 0 only when the whole wave is past M
+  uint32_t aoff[16];
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt) {
-    int64_t r = m0 + 32 * mt + jl;
-    if (r >= g.M) r = g.M - 1;
-    arow[mt] = g.a + r * g.lda + 32 * grp;
+  for (int i = 0; i < 16; ++i) {
+    const int rr = 8 * i + (lane >> 3);
+    int rel = rr + skip;
+    if (rel > avail - 1) rel = avail - 1;
+    const int u = (lane & 7) ^ (rr & 7);
+    aoff[i] = (uint32_t)rel * lda2 + 16u * (uint32_t)u;
   }
 
   Producer prod;
@@ -269,50 +300,62 @@ __global__ void __launch_bounds__(kGemmThreads, 1) nf4_gemm_kernel(const GemmArg
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[mt][nt][v] = 0.0f;
 
-  u32x4 A[4][4];
+  u32x4 *a0w = g_lds_a0 + wave * 1024;
+  u32x4 *a1w = g_lds_a1 + wave * 1024;
+
+  // Prologue: activation tile of step 0 (DMA), weight tile of step 0
+  // (dequantized into b0), packed weights of step 1 in registers.
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-    for (int s = 0; s < 4; ++s)
-      A[mt][s] = *reinterpret_cast<const u32x4 *>(arow[mt] + 8 * s);
+  for (int i = 0; i < 16; ++i)
+    __builtin_amdgcn_global_load_lds(abase + aoff[i], (lds_void_t *)(a0w + i * 64), 16, 0, 0);
   {
     u32x4 w0;
-    float a0;
-    prod.load(g, 0, w0, a0);
-    prod.store(lds[0], w0, a0);
+    float s0;
+    prod.load(g, 0, w0, s0);
+    prod.store(g_lds_b0, w0, s0);
   }
-  // wc/ac: weights of step t+1 (dequantized during step t); wn/an: step t+2.
   u32x4 wc, wn;
   float ac, an;
   prod.load(g, nsteps > 1 ? 1 : 0, wc, ac);
+  __builtin_amdgcn_s_waitcnt(0);  // the DMA of step 0 has landed in LDS
   __syncthreads();
 
-  // One loop body for every step.  The last step's "next" work reads clamped
-  // (valid) addresses and writes the LDS buffer nobody reads again.
+  // One loop body for every step; the buffers alternate by step parity.
+  // The last step's "next" work reads clamped (valid) addresses and fills
+  // buffers nobody reads again.
 #pragma unroll 1
   for (int64_t t = 0; t < nsteps; ++t) {
-    const int buf = (int)(t & 1);
-    gemm_step<Producer>(g, prod, acc, A, wc, ac, wn, an, arow, lds[buf], lds[buf ^ 1], t, nsteps,
-                        jl, grp);
+    const bool odd = (t & 1) != 0;
+    gemm_step<Producer>(g, prod, acc, odd ? a1w : a0w, odd ? a0w : a1w, odd ? g_lds_b1 : g_lds_b0,
+                        odd ? g_lds_b0 : g_lds_b1, abase, aoff, wc, ac, wn, an, t, nsteps, jl,
+                        grp);
+    // Next step's activation tile (direct-to-LDS) and weight tile complete.
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     wc = wn;
     ac = an;
   }
 
-  // Epilogue: fp32 -> bf16 (RNE), lane l writes column o0 + 32nt + l%32.
+  // Epilogue: fp32 -> bf16 (RNE).  Lane l holds column o0 + 32nt + l%32 of
+  // rows m0 + 32mt + 8(v/4) + 4g + v%4; one 64-bit base pointer per lane,
+  // uniform row offsets, 32-bit bounds.
+  const int64_t row0 = m0 + 4 * grp;
+  const int64_t rl = g.M - row0;
+  const int64_t cl = g.O - (o0 + jl);
+  const int32_t rlim = (int32_t)(rl < 0 ? 0 : (rl > (1 << 30) ? (1 << 30) : rl));
+  const int32_t clim = (int32_t)(cl < 0 ? 0 : (cl > (1 << 30) ? (1 << 30) : cl));
+  uint16_t *obase = g.out + (row0 < g.M ? row0 : 0) * g.ldo + o0 + jl;
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt) {
-      const int64_t col = o0 + 32 * nt + jl;
-      if (col >= g.O) continue;
+    for (int v = 0; v < 16; ++v) {
+      const int r = 32 * mt + 8 * (v >> 2) + (v & 3);
+      if (r < rlim) {
+        uint16_t *orow = obase + (int64_t)r * g.ldo;
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int64_t row = m0 + 32 * mt + 8 * (v >> 2) + 4 * grp + (v & 3);
-        if (row < g.M) {
-          const __bf16 h = (__bf16)acc[mt][nt][v];
-          g.out[row * g.ldo + col] = __builtin_bit_cast(uint16_t, h);
-        }
+        for (int nt = 0; nt < 4; ++nt)
+          if (32 * nt < clim)
+            orow[32 * nt] = __builtin_bit_cast(uint16_t, (__bf16)acc[mt][nt][v]);
       }
     }
 }
