@@ -5,12 +5,17 @@ layer (q/k/v/o 4096x4096, gate/up 11008x4096, down
 4096x11008; block 64; absmax double-quantized to uint8 in groups of 256 with
 an fp32 scale), one grouped launch per step, inputs resident in HBM.
 ``value`` = algorithmic bytes (packed + uint8 absmax + fp32 scales + bf16 out
-= 509,149,440 B) / average step time, in GB/s.
+= 509,149,440 B) / average kernel time (HIP events on the launch stream), GB/s.
 
-Also reported: the fused NF4 GEMM (forward X.W^T and input-gradient dY.W) at
-the 7B and 70B layer shapes, in TFLOP/s, each with its roofline fraction.
+Also reported under "gemm": the NF4-dequant-fused GEMM in TFLOP/s against the
+bf16 dense MFMA peak,
+  config 3: 4096 tokens x (gate, up 11008x4096; down 4096x11008), forward;
+  config 4: one 70B layer (q/o 8192x8192, k/v 1024x8192, gate/up 28672x8192,
+            down 8192x28672; double-quant), 8192 tokens: forward +
+            recompute-forward + input-gradient over all 7 matrices.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+                       [--workload all|dequant|gemm] [--copy-calibration]
 """
 from __future__ import annotations
 
@@ -21,10 +26,15 @@ import sys
 import time
 
 HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, 8 TB/s
-BF16_PEAK_TFLOPS = 2500.0    # MI355X dense bf16 MFMA
+BF16_PEAK_TFLOPS = 2500.0    # MI355X dense bf16 MFMA, 2.5 PFLOP/s
+ROOT = os.path.dirname(os.path.abspath(__file__))
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "dequant_7b_layer_pmc.txt")
 
 LAYER_7B = [("q", 4096, 4096), ("k", 4096, 4096), ("v", 4096, 4096), ("o", 4096, 4096),
             ("gate", 11008, 4096), ("up", 11008, 4096), ("down", 4096, 11008)]
+GEMM_7B = [("gate", 11008, 4096), ("up", 11008, 4096), ("down", 4096, 11008)]
+LAYER_70B = [("q", 8192, 8192), ("k", 1024, 8192), ("v", 1024, 8192), ("o", 8192, 8192),
+             ("gate", 28672, 8192), ("up", 28672, 8192), ("down", 8192, 28672)]
 
 
 def algorithmic_bytes_dq(shapes, bs=64, group=256) -> int:
@@ -43,14 +53,21 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
-                    help="approximate CPU time budget of the cpu_baseline sample")
+                    help="approximate CPU time budget of the dequant cpu_baseline sample")
+    ap.add_argument("--workload", choices=["all", "dequant", "gemm"], default="all")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain 1 GiB device-to-device copy (PMC byte calibration)")
     return ap.parse_args()
 
 
-def build_layer(torch, nf4, seed=2):
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def make_weights(torch, nf4, shapes, seed):
     g = torch.Generator(device="cuda").manual_seed(seed)
     ws = []
-    for _, r, c in LAYER_7B:
+    for _, r, c in shapes:
         wf = torch.randn(r, c, device="cuda", generator=g) * 0.02
         ws.append(nf4.quantize_weight(wf, double_quant=True))
         del wf
@@ -58,39 +75,48 @@ def build_layer(torch, nf4, seed=2):
     return ws
 
 
-def time_dequant(torch, nf4, ws, steps, warmup):
-    outs = [torch.empty(w.shape, dtype=torch.bfloat16, device="cuda") for w in ws]
+def timed(torch, fn, steps, warmup):
+    """Average ms of fn() over `steps` runs, HIP events on the current stream
+    (the stream every call here launches on)."""
     for _ in range(warmup):
-        nf4.dequant_batch(ws, outs)
+        fn()
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     start.record()
     for _ in range(steps):
-        nf4.dequant_batch(ws, outs)
+        fn()
     end.record()
     torch.cuda.synchronize()
-    return start.elapsed_time(end) / steps, outs
+    return start.elapsed_time(end) / steps
 
 
-def cpu_baseline(ws, budget_s):
+def read_traffic():
+    """HBM bytes per dequant launch from the committed rocprofv3 PMC summary."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(float(line.split(":", 1)[1].strip()))
+    except OSError:
+        pass
+    return None
+
+
+def cpu_baseline_dequant(ws, budget_s):
     """The oracle's dequant (scalar C restatement of shard_engine/src/nf4.rs:37-83,
     f16 out as the reference) on the host, single thread, on a bounded sample:
     whole matrices of the same layer until ~budget_s of CPU time."""
-    import numpy as np
     import oracle
-    import torch
-    done_bytes, elapsed, mats = 0, 0.0, 0
-    i = 0
+    done_bytes, elapsed, mats, i = 0, 0.0, 0, 0
     while elapsed < budget_s and mats < 64:
         w = ws[i % len(ws)]
         pk = w.packed.cpu().numpy()
         q = w.absmax_q.cpu().numpy()
         sc = w.absmax_scale.cpu().numpy()
-        n = w.numel
         t0 = time.perf_counter()
         am = oracle.dq_decode(q, sc, w.dq_group)
-        oracle.dequant_f16(pk, am, n, w.block_size)
+        oracle.dequant_f16(pk, am, w.numel, w.block_size)
         elapsed += time.perf_counter() - t0
         done_bytes += algorithmic_bytes_dq([("", w.shape[0], w.shape[1])])
         mats += 1
@@ -101,52 +127,167 @@ def cpu_baseline(ws, budget_s):
         "cores": 1,
         "kind": "port",
         "sample": f"{mats} whole matrices of the same 7B layer ({done_bytes} algorithmic bytes, "
-                  f"{elapsed:.1f} s), oracle dq-decode + f16 dequant, 1 thread",
+                  f"{elapsed:.1f} s): oracle double-quant decode + f16 dequant, 1 thread",
     }
+
+
+def cpu_baseline_gemm(rows=8):
+    """The oracle's matmul_tb (doublepass/src/math.rs:9-21, fp32 triple loop,
+    1 thread) on a `rows`-row slice of the 7B gate GEMM; cost is linear in M."""
+    import numpy as np
+    import oracle
+    n, k = 11008, 4096
+    a = oracle.gen_normal(11, rows * k, 1.0).reshape(rows, k)
+    b = oracle.gen_normal(12, n * k, 0.02).reshape(n, k)
+    t0 = time.perf_counter()
+    oracle.matmul_tb(a, b)
+    dt = time.perf_counter() - t0
+    fl = 2.0 * rows * n * k
+    return {"value": round(fl / dt / 1e12, 6), "unit": "TFLOP/s", "cores": 1, "kind": "port",
+            "sample": f"{rows} rows x gate 11008x4096 ({dt:.2f} s); time scales linearly in M"}
+
+
+def bench_dequant(torch, nf4, args):
+    log("building the 7B layer (quantize + double-quant on device)")
+    ws = make_weights(torch, nf4, LAYER_7B, seed=2)
+    outs = [torch.empty(w.shape, dtype=torch.bfloat16, device="cuda") for w in ws]
+    log("timing the grouped dequant")
+    ms = timed(torch, lambda: nf4.dequant_batch(ws, outs), args.steps, args.warmup)
+    return ws, ms
+
+
+def bench_gemm(torch, nf4, gemm, args):
+    res = {}
+    # Config 3: 7B MLP GEMMs, forward, 4096 tokens.
+    log("config 3: 7B gate/up/down forward")
+    ws = make_weights(torch, nf4, GEMM_7B, seed=3)
+    g = torch.Generator(device="cuda").manual_seed(30)
+    x = torch.randn(4096, 4096, device="cuda", generator=g).to(torch.bfloat16)
+    xd = torch.randn(4096, 11008, device="cuda", generator=g).to(torch.bfloat16)
+    ys = [torch.empty(4096, w.shape[0], dtype=torch.bfloat16, device="cuda") for w in ws]
+    acts = [x, x, xd]
+
+    def cfg3():
+        for a, w, y in zip(acts, ws, ys):
+            gemm.linear_fwd(a, w, y)
+    steps = max(3, args.steps // 5)
+    ms3 = timed(torch, cfg3, steps, 2)
+    fl3 = sum(2.0 * 4096 * w.shape[0] * w.shape[1] for w in ws)
+    tf3 = fl3 / (ms3 * 1e-3) / 1e12
+    res["config3_7b_mlp_fwd"] = {"tflops": round(tf3, 1), "ms": round(ms3, 4), "flop": fl3,
+                                 "frac_of_bf16_peak": round(tf3 / BF16_PEAK_TFLOPS, 4)}
+    del ws, x, xd, ys, acts
+    torch.cuda.empty_cache()
+
+    # Config 4: a 70B layer, forward + recompute-forward + dgrad, 8192 tokens.
+    log("config 4: 70B layer forward + recompute + dgrad")
+    M = 8192
+    ws = make_weights(torch, nf4, LAYER_70B, seed=4)
+    g = torch.Generator(device="cuda").manual_seed(40)
+    h = torch.randn(M, 8192, device="cuda", generator=g).to(torch.bfloat16)
+    hid = torch.randn(M, 28672, device="cuda", generator=g).to(torch.bfloat16)
+    ins = [h, h, h, h, h, h, hid]                    # q k v o gate up : down
+    ys = [torch.empty(M, w.shape[0], dtype=torch.bfloat16, device="cuda") for w in ws]
+    dys = [torch.randn(M, w.shape[0], device="cuda", generator=g).to(torch.bfloat16) for w in ws]
+    dxs = [torch.empty(M, w.shape[1], dtype=torch.bfloat16, device="cuda") for w in ws]
+
+    def fwd_pass():
+        for a, w, y in zip(ins, ws, ys):
+            gemm.linear_fwd(a, w, y)
+
+    def dgrad_pass():
+        for dy, w, dx in zip(dys, ws, dxs):
+            gemm.linear_dgrad(dy, w, dx)
+
+    def layer_step():
+        fwd_pass()      # forward
+        fwd_pass()      # double-pass recompute forward
+        dgrad_pass()    # input gradient
+
+    steps4 = max(2, args.steps // 10)
+    ms_f = timed(torch, fwd_pass, steps4, 1)
+    ms_d = timed(torch, dgrad_pass, steps4, 1)
+    ms_l = timed(torch, layer_step, steps4, 1)
+    fl_pass = sum(2.0 * M * w.shape[0] * w.shape[1] for w in ws)
+    per = {}
+    for (name, _, _), a, w, y, dy, dx in zip(LAYER_70B, ins, ws, ys, dys, dxs):
+        f = 2.0 * M * w.shape[0] * w.shape[1]
+        mf = timed(torch, lambda: gemm.linear_fwd(a, w, y), steps4, 1)
+        md = timed(torch, lambda: gemm.linear_dgrad(dy, w, dx), steps4, 1)
+        per[name] = {"fwd_tflops": round(f / (mf * 1e-3) / 1e12, 1),
+                     "dgrad_tflops": round(f / (md * 1e-3) / 1e12, 1)}
+    tf_l = 3 * fl_pass / (ms_l * 1e-3) / 1e12
+    res["config4_70b_layer"] = {
+        "tflops": round(tf_l, 1), "ms_per_layer_step": round(ms_l, 3),
+        "flop_per_pass": fl_pass, "passes": 3,
+        "frac_of_bf16_peak": round(tf_l / BF16_PEAK_TFLOPS, 4),
+        "fwd_pass_tflops": round(fl_pass / (ms_f * 1e-3) / 1e12, 1),
+        "dgrad_pass_tflops": round(fl_pass / (ms_d * 1e-3) / 1e12, 1),
+        "per_matrix": per,
+    }
+    return res
+
+
+def copy_calibration(torch):
+    """A plain device copy of exactly 1 GiB read + 1 GiB written (the known
+    byte count that rocprofv3's FETCH_SIZE / WRITE_SIZE are scaled against)."""
+    n = 1 << 30
+    a = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes_each_way": n, "launches": 3}), flush=True)
 
 
 def main():
     args = parse()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU: every GPU box here has one GPU; "
+        print(json.dumps({"error": "this build runs on one GPU (every GPU box here has one); "
                                    "bench.py --gpus N with N > 1 is not supported"}))
         sys.exit(2)
     import torch
-    from aethelstream_amd import nf4
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no GPU visible"}))
         sys.exit(1)
-    print("[bench] building 7B layer (quantize + double-quant on device)", file=sys.stderr, flush=True)
-    ws = build_layer(torch, nf4)
-    print("[bench] timing dequant", file=sys.stderr, flush=True)
-    ms, _ = time_dequant(torch, nf4, ws, args.steps, args.warmup)
-    nbytes = algorithmic_bytes_dq(LAYER_7B)
-    gbs = nbytes / (ms * 1e-3) / 1e9
+    if args.copy_calibration:
+        copy_calibration(torch)
+        return
+    from aethelstream_amd import gemm, nf4
+
     line = {
         "metric": "NF4 dequant HBM GB/s (% peak); NF4-fused GEMM TFLOP/s at 7B/70B layer shapes",
-        "value": round(gbs, 2),
-        "unit": "GB/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms, 5),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic (torch.randn * 0.02 weights, quantized on device)",
+        "value": None, "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": None, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic: torch.randn weights (sigma 0.02) quantized on device, "
+                "randn activations",
         "config": {"workload": "config2: NF4 dequant to bf16 of one Llama-7B decoder layer "
                                "(q/k/v/o 4096x4096, gate/up 11008x4096, down 4096x11008), "
-                               "block 64, double-quant uint8 absmax in groups of 256, "
-                               "one grouped launch",
+                               "block 64, double-quant uint8 absmax in groups of 256, one "
+                               "grouped launch per step",
                    "elements": sum(r * c for _, r, c in LAYER_7B),
-                   "algorithmic_bytes": nbytes},
-        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+                   "algorithmic_bytes": algorithmic_bytes_dq(LAYER_7B)},
     }
-    if not args.no_cpu_baseline:
-        print("[bench] cpu baseline", file=sys.stderr, flush=True)
-        line["cpu_baseline"] = cpu_baseline(ws, args.cpu_seconds)
+    ws = None
+    if args.workload in ("all", "dequant"):
+        ws, ms = bench_dequant(torch, nf4, args)
+        nbytes = algorithmic_bytes_dq(LAYER_7B)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        line["value"] = round(gbs, 2)
+        line["ms_per_step"] = round(ms, 5)
+        line["roofline"] = {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
+                            "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                            "traffic": read_traffic()}
+    if args.workload in ("all", "gemm"):
+        line["gemm"] = bench_gemm(torch, nf4, gemm, args)
+        line["gemm"]["peak_tflops"] = BF16_PEAK_TFLOPS
+    if not args.no_cpu_baseline and ws is not None:
+        log("cpu baseline (oracle, 1 thread)")
+        line["cpu_baseline"] = cpu_baseline_dequant(ws, args.cpu_seconds)
+        if args.workload == "all":
+            line["cpu_baseline_gemm"] = cpu_baseline_gemm()
     print(json.dumps(line), flush=True)
 
 
