@@ -1,0 +1,152 @@
+// nf4_stream.hip - streamed layer stack on one GPU: pinned host layers, a
+// two-slot device double buffer fed by a copy stream, events between the
+// copy and compute streams.
+//
+// Mirrors flowcast's VramDoubleBuffer (flowcast/src/vram_double_buffer.rs:
+// 196-301) with the real transfer the reference only declares
+// (ramflow/src/cuda_bridge/bindings.rs:115-125,304-316):
+//   advance(layer, src):  the copy stream waits until the staging slot is no
+//   longer read by the compute stream, copies src into it (hipMemcpyAsync
+//   H2D), records the slot's ready event, swaps the slots and returns the
+//   new compute slot with its ready event.  The consumer makes its compute
+//   stream wait on that event before reading the slot (ready.rs:16-19,43-51)
+//   and calls release(slot) after enqueuing the kernels that read it.
+// The buffer handed out at call N is overwritten at call N+2
+// (vram_double_buffer.rs:258-262); release() turns that invariant into an
+// event the copy stream waits on, so the host may run ahead of the GPU.
+#include "abi_common.hpp"
+
+#include <new>
+
+struct nf4s_dbuf {
+  void *slot[2];          // device buffers
+  hipEvent_t ready[2];    // copy into the slot complete
+  hipEvent_t freed[2];    // last reader of the slot complete
+  bool freed_valid[2];    // a release was recorded for the slot
+  int64_t capacity;
+  int staging;            // index of slot_b (the next copy target)
+  hipStream_t copy;
+};
+
+namespace nf4s {
+
+static int32_t hip_fail(hipError_t e, const char *what) {
+  return fail(NF4S_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+}  // namespace nf4s
+
+using namespace nf4s;
+
+extern "C" {
+
+int32_t nf4s_host_alloc(int64_t bytes, void **out) {
+  if (out == nullptr || bytes <= 0) return fail(NF4S_ERR_INVALID_ARGUMENT, "bad host_alloc args");
+  *out = nullptr;
+  // Pinned (page-locked) host memory allocated as such; no hipHostRegister.
+  const hipError_t e = hipHostMalloc(out, (size_t)bytes, hipHostMallocDefault);
+  if (e != hipSuccess) return hip_fail(e, "hipHostMalloc");
+  return NF4S_OK;
+}
+
+int32_t nf4s_host_free(void *p) {
+  if (p == nullptr) return NF4S_OK;
+  const hipError_t e = hipHostFree(p);
+  if (e != hipSuccess) return hip_fail(e, "hipHostFree");
+  return NF4S_OK;
+}
+
+int32_t nf4s_dbuf_create(int64_t slot_bytes, nf4s_dbuf **out) {
+  if (out == nullptr || slot_bytes <= 0)
+    return fail(NF4S_ERR_INVALID_ARGUMENT, "bad dbuf_create args");
+  *out = nullptr;
+  nf4s_dbuf *d = new (std::nothrow) nf4s_dbuf();
+  if (d == nullptr) return fail(NF4S_ERR_INVALID_ARGUMENT, "out of host memory");
+  d->capacity = slot_bytes;
+  d->staging = 1;
+  hipError_t e = hipSuccess;
+  for (int i = 0; i < 2 && e == hipSuccess; ++i) e = hipMalloc(&d->slot[i], (size_t)slot_bytes);
+  for (int i = 0; i < 2 && e == hipSuccess; ++i)
+    e = hipEventCreateWithFlags(&d->ready[i], hipEventDisableTiming);
+  for (int i = 0; i < 2 && e == hipSuccess; ++i)
+    e = hipEventCreateWithFlags(&d->freed[i], hipEventDisableTiming);
+  if (e == hipSuccess) e = hipStreamCreateWithFlags(&d->copy, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    const int32_t rc = hip_fail(e, "dbuf_create");
+    for (int i = 0; i < 2; ++i) {
+      if (d->slot[i]) (void)hipFree(d->slot[i]);
+      if (d->ready[i]) (void)hipEventDestroy(d->ready[i]);
+      if (d->freed[i]) (void)hipEventDestroy(d->freed[i]);
+    }
+    delete d;
+    return rc;
+  }
+  *out = d;
+  return NF4S_OK;
+}
+
+int32_t nf4s_dbuf_destroy(nf4s_dbuf *d) {
+  if (d == nullptr) return NF4S_OK;
+  hipError_t e = hipStreamSynchronize(d->copy);
+  for (int i = 0; i < 2; ++i) {
+    if (d->freed_valid[i]) (void)hipEventSynchronize(d->freed[i]);
+    (void)hipFree(d->slot[i]);
+    (void)hipEventDestroy(d->ready[i]);
+    (void)hipEventDestroy(d->freed[i]);
+  }
+  (void)hipStreamDestroy(d->copy);
+  delete d;
+  if (e != hipSuccess) return hip_fail(e, "dbuf_destroy");
+  return NF4S_OK;
+}
+
+int64_t nf4s_dbuf_capacity(const nf4s_dbuf *d) { return d ? d->capacity : 0; }
+
+// vram_double_buffer.rs:263-301.
+int32_t nf4s_dbuf_advance(nf4s_dbuf *d, uint32_t layer_idx, const void *src, int64_t len,
+                          void **dev_ptr, void **ready_event) {
+  if (d == nullptr || dev_ptr == nullptr || ready_event == nullptr)
+    return fail(NF4S_ERR_INVALID_ARGUMENT, "bad dbuf_advance args");
+  if (len < 0 || (len > 0 && src == nullptr))
+    return fail(NF4S_ERR_INVALID_ARGUMENT, "bad source buffer");
+  if (len > d->capacity)  // vram_double_buffer.rs:269-275, same message
+    return fail(NF4S_ERR_INVALID_ARGUMENT, "layer %u: src len %lld B exceeds slot capacity %lld B",
+                layer_idx, (long long)len, (long long)d->capacity);
+  const int b = d->staging;
+  hipError_t e = hipSuccess;
+  if (d->freed_valid[b]) e = hipStreamWaitEvent(d->copy, d->freed[b], 0);
+  if (e == hipSuccess && len > 0)
+    e = hipMemcpyAsync(d->slot[b], src, (size_t)len, hipMemcpyHostToDevice, d->copy);
+  if (e == hipSuccess) e = hipEventRecord(d->ready[b], d->copy);
+  if (e != hipSuccess) return hip_fail(e, "dbuf_advance");
+  d->freed_valid[b] = false;
+  d->staging = b ^ 1;  // swap: the filled slot becomes the compute slot
+  *dev_ptr = d->slot[b];
+  *ready_event = reinterpret_cast<void *>(d->ready[b]);
+  return NF4S_OK;
+}
+
+// Records that everything enqueued so far on `compute_stream` is the last
+// use of the slot at `dev_ptr` (a pointer nf4s_dbuf_advance returned); the
+// copy that refills that slot waits for it.
+int32_t nf4s_dbuf_release(nf4s_dbuf *d, const void *dev_ptr, void *compute_stream) {
+  if (d == nullptr) return fail(NF4S_ERR_INVALID_ARGUMENT, "dbuf is NULL");
+  int i = -1;
+  for (int k = 0; k < 2; ++k)
+    if (d->slot[k] == dev_ptr) i = k;
+  if (i < 0) return fail(NF4S_ERR_INVALID_ARGUMENT, "pointer is not a slot of this buffer");
+  const hipError_t e = hipEventRecord(d->freed[i], as_stream(compute_stream));
+  if (e != hipSuccess) return hip_fail(e, "dbuf_release");
+  d->freed_valid[i] = true;
+  return NF4S_OK;
+}
+
+int32_t nf4s_stream_wait_event(void *stream, void *event) {
+  if (event == nullptr) return fail(NF4S_ERR_INVALID_ARGUMENT, "event is NULL");
+  const hipError_t e =
+      hipStreamWaitEvent(as_stream(stream), reinterpret_cast<hipEvent_t>(event), 0);
+  if (e != hipSuccess) return hip_fail(e, "stream_wait_event");
+  return NF4S_OK;
+}
+
+}  // extern "C"

@@ -14,8 +14,13 @@ bf16 dense MFMA peak,
             down 8192x28672; double-quant), 8192 tokens: forward +
             recompute-forward + input-gradient over all 7 matrices.
 
+Under "stream", config 5: 80 70B layers in pinned host memory streamed
+through a two-slot device buffer (H2D on a copy stream) while the previous
+layer's forward GEMMs run, 4096 tokens: layers/s, H2D GB/s, overlap.
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
-                       [--workload all|dequant|gemm] [--copy-calibration]
+                       [--workload all|dequant|gemm|stream] [--stream-layers L]
+                       [--copy-calibration]
 """
 from __future__ import annotations
 
@@ -54,7 +59,9 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="approximate CPU time budget of the dequant cpu_baseline sample")
-    ap.add_argument("--workload", choices=["all", "dequant", "gemm"], default="all")
+    ap.add_argument("--workload", choices=["all", "dequant", "gemm", "stream"], default="all")
+    ap.add_argument("--stream-layers", type=int, default=80,
+                    help="config 5: number of 70B layers held in pinned host memory")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device-to-device copy (PMC byte calibration)")
     return ap.parse_args()
@@ -228,6 +235,80 @@ def bench_gemm(torch, nf4, gemm, args):
     return res
 
 
+def bench_stream(torch, nf4, gemm, nlayers, M=4096):
+    """Config 5: `nlayers` 70B-shaped NF4 layers (double-quant) in pinned host
+    memory, each copied H2D on a side stream while the previous layer's
+    fused forward GEMMs run on the compute stream (flowcast's VRAM double
+    buffer), M tokens."""
+    from aethelstream_amd import stream as st
+    layout = st.LayerLayout(LAYER_70B)
+    t0 = time.perf_counter()
+    distinct = [make_weights(torch, nf4, LAYER_70B, seed=100 + i) for i in range(4)]
+    host = []
+    for l in range(nlayers):
+        pb = st.PinnedBuffer(layout.nbytes)
+        layout.pack_into(pb.tensor, distinct[l % len(distinct)])
+        host.append(pb)
+    resident = torch.empty(layout.nbytes, dtype=torch.uint8, device="cuda")
+    resident.copy_(host[0].tensor)
+    del distinct
+    torch.cuda.synchronize()
+    setup_s = time.perf_counter() - t0
+    dbuf = st.VramDoubleBuffer(layout.nbytes)
+    g = torch.Generator(device="cuda").manual_seed(50)
+    x = torch.randn(M, 8192, device="cuda", generator=g).to(torch.bfloat16)
+    hid = torch.randn(M, 28672, device="cuda", generator=g).to(torch.bfloat16)
+    ins = [x, x, x, x, x, x, hid]
+    outs = [torch.empty(M, r, dtype=torch.bfloat16, device="cuda") for _, r, _ in LAYER_70B]
+    comp = torch.cuda.current_stream()
+
+    def compute(l, views):
+        for a, w, y in zip(ins, views, outs):
+            gemm.linear_fwd(a, w, y)
+
+    def wall(fn):
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        fn()
+        torch.cuda.synchronize()
+        return time.perf_counter() - t
+
+    def copies_only():
+        for l in range(nlayers):
+            p, ev = dbuf.advance(l, host[l].ptr, layout.nbytes)
+            st.stream_wait_event(comp, ev)
+            dbuf.release(p, comp)
+
+    rviews = layout.views(resident.data_ptr())
+
+    def compute_only():
+        for l in range(nlayers):
+            compute(l, rviews)
+
+    def streamed():
+        st.run_stack(host, layout, dbuf, compute, comp)
+
+    wall(streamed)                      # warm-up
+    t_h2d = wall(copies_only)
+    t_comp = wall(compute_only)
+    t_tot = wall(streamed)
+    fl = nlayers * sum(2.0 * M * r * c for _, r, c in LAYER_70B)
+    dbuf.close()
+    for pb in host:
+        pb.close()
+    return {
+        "layers": nlayers, "tokens": M, "layer_bytes": layout.nbytes,
+        "layers_per_s": round(nlayers / t_tot, 2),
+        "ms_per_layer": round(1e3 * t_tot / nlayers, 3),
+        "h2d_gbs": round(nlayers * layout.nbytes / t_h2d / 1e9, 2),
+        "t_h2d_s": round(t_h2d, 4), "t_compute_s": round(t_comp, 4), "t_total_s": round(t_tot, 4),
+        "overlap": round((t_h2d + t_comp - t_tot) / min(t_h2d, t_comp), 3),
+        "tflops_streamed": round(fl / t_tot / 1e12, 1),
+        "tflops_resident": round(fl / t_comp / 1e12, 1),
+        "setup_s": round(setup_s, 1),
+    }
+
+
 def copy_calibration(torch):
     """A plain device copy of exactly 1 GiB read + 1 GiB written (the known
     byte count that rocprofv3's FETCH_SIZE / WRITE_SIZE are scaled against)."""
@@ -283,6 +364,12 @@ def main():
     if args.workload in ("all", "gemm"):
         line["gemm"] = bench_gemm(torch, nf4, gemm, args)
         line["gemm"]["peak_tflops"] = BF16_PEAK_TFLOPS
+    if args.workload in ("all", "stream"):
+        log(f"config 5: {args.stream_layers} streamed 70B layers")
+        try:
+            line["stream"] = bench_stream(torch, nf4, gemm, args.stream_layers)
+        except Exception as e:  # reported, the rest of the line still prints
+            line["stream"] = {"error": repr(e)}
     if not args.no_cpu_baseline and ws is not None:
         log("cpu baseline (oracle, 1 thread)")
         line["cpu_baseline"] = cpu_baseline_dequant(ws, args.cpu_seconds)

@@ -132,6 +132,46 @@ int32_t nf4s_gemm_fwd(const uint16_t *x, const nf4s_tensor *w, int64_t m,
 int32_t nf4s_gemm_dgrad(const uint16_t *dy, const nf4s_tensor *w, int64_t m,
                         int64_t n, int64_t k, uint16_t *dx, void *stream);
 
+/* ---------------------------------------------------------------------------
+ * Streamed layer stack (one GPU).  Layers wait in pinned host memory and are
+ * copied into a two-slot device double buffer on a dedicated copy stream.
+ * ------------------------------------------------------------------------- */
+
+/* Pinned (page-locked) host memory of `bytes`; replaces PinnedBuffer::alloc
+ * (ramflow/src/allocator/pinned.rs:306) for the H2D source buffers. */
+int32_t nf4s_host_alloc(int64_t bytes, void **out);
+int32_t nf4s_host_free(void *p);
+
+/* Two device slots of `slot_bytes`, a copy stream and per-slot events;
+ * replaces VramDoubleBuffer::new (flowcast/src/vram_double_buffer.rs:230-237).
+ * Allocates; the other dbuf calls do not. */
+typedef struct nf4s_dbuf nf4s_dbuf;
+int32_t nf4s_dbuf_create(int64_t slot_bytes, nf4s_dbuf **out);
+int32_t nf4s_dbuf_destroy(nf4s_dbuf *d);
+int64_t nf4s_dbuf_capacity(const nf4s_dbuf *d);
+
+/*
+ * VramDoubleBuffer::advance (flowcast/src/vram_double_buffer.rs:263-301):
+ * copies `len` bytes of host `src` (pinned for an asynchronous copy) into the
+ * staging slot on the copy stream, records the slot's ready event, swaps the
+ * slots and returns the new compute slot and its event.  The consumer must
+ * make its compute stream wait on `*ready_event` (nf4s_stream_wait_event)
+ * before reading `*dev_ptr` (flowcast/src/ready.rs:16-19,43-51).  Fails
+ * when len exceeds the slot capacity (vram_double_buffer.rs:269-275).  The
+ * slot returned at call N is refilled at call N+2, after the copy stream has
+ * waited for the release recorded for it.
+ */
+int32_t nf4s_dbuf_advance(nf4s_dbuf *d, uint32_t layer_idx, const void *src,
+                          int64_t len, void **dev_ptr, void **ready_event);
+
+/* Records that everything enqueued so far on `compute_stream` is the last use
+ * of the slot at `dev_ptr` (returned by nf4s_dbuf_advance); the copy that
+ * refills that slot waits for this. */
+int32_t nf4s_dbuf_release(nf4s_dbuf *d, const void *dev_ptr, void *compute_stream);
+
+/* hipStreamWaitEvent on a ready event returned by nf4s_dbuf_advance. */
+int32_t nf4s_stream_wait_event(void *stream, void *event);
+
 #ifdef __cplusplus
 }
 #endif
