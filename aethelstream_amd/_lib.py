@@ -18,6 +18,11 @@ NF4S_ERR_PACKED_TOO_SMALL = 3
 NF4S_ERR_MISALIGNED = 4
 NF4S_ERR_UNSUPPORTED_SHAPE = 5
 NF4S_ERR_HIP = 6
+NF4S_ERR_IO = 7
+NF4S_ERR_JSON = 8
+NF4S_ERR_LAYER_NOT_FOUND = 9
+NF4S_ERR_PARAM_NOT_FOUND = 10
+NF4S_ERR_MALFORMED_INDEX = 11
 
 
 class Nf4sTensor(ctypes.Structure):
@@ -33,6 +38,25 @@ class Nf4sTensor(ctypes.Structure):
         ("scale_len", ctypes.c_int64),
         ("block_size", ctypes.c_int32),
         ("dq_group", ctypes.c_int32),
+    ]
+
+
+class Nf4sParamInfo(ctypes.Structure):
+    """Mirror of ``struct nf4s_param_info`` (include/nf4stream.h)."""
+
+    _fields_ = [
+        ("shape", ctypes.c_int64 * 8),
+        ("ndim", ctypes.c_int32),
+        ("precision", ctypes.c_int32),
+        ("numel", ctypes.c_int64),
+        ("byte_length", ctypes.c_int64),
+        ("absmax_len", ctypes.c_int64),
+        ("scale_len", ctypes.c_int64),
+        ("block_size", ctypes.c_int32),
+        ("dq_group", ctypes.c_int32),
+        ("out_elems", ctypes.c_int64),
+        ("precision_str", ctypes.c_char * 16),
+        ("dtype_str", ctypes.c_char * 16),
     ]
 
 
@@ -61,6 +85,13 @@ SIGNATURES = {
                                  ctypes.POINTER(_P)]),
     "nf4s_dbuf_release": (_I32, [_P, _P, _P]),
     "nf4s_stream_wait_event": (_I32, [_P, _P]),
+    "nf4s_loader_open": (_I32, [ctypes.c_char_p, ctypes.POINTER(_P)]),
+    "nf4s_loader_close": (_I32, [_P]),
+    "nf4s_loader_param_info": (_I32, [_P, ctypes.c_char_p, ctypes.POINTER(Nf4sParamInfo)]),
+    "nf4s_loader_load_layer": (_I32, [_P, ctypes.c_uint32, ctypes.POINTER(_P),
+                                      ctypes.POINTER(_I64)]),
+    "nf4s_loader_load_param_f16": (_I32, [_P, ctypes.c_char_p, _P, _I64, _P]),
+    "nf4s_loader_load_param_nf4": (_I32, [_P, ctypes.c_char_p, _P, _P, _P, _P]),
 }
 
 _lib = None

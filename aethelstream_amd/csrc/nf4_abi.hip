@@ -66,6 +66,11 @@ const char *nf4s_strerror(int32_t status) {
     case NF4S_ERR_MISALIGNED: return "misaligned pointer";
     case NF4S_ERR_UNSUPPORTED_SHAPE: return "unsupported shape";
     case NF4S_ERR_HIP: return "HIP runtime error";
+    case NF4S_ERR_IO: return "I/O error";
+    case NF4S_ERR_JSON: return "JSON parse error";
+    case NF4S_ERR_LAYER_NOT_FOUND: return "layer index not found in layer registry";
+    case NF4S_ERR_PARAM_NOT_FOUND: return "parameter not found in shard index";
+    case NF4S_ERR_MALFORMED_INDEX: return "malformed index entry";
     default: return "unknown status";
   }
 }

@@ -32,7 +32,12 @@ enum nf4s_status {
     NF4S_ERR_PACKED_TOO_SMALL = 3,   /* nf4.rs:52-57 MalformedIndex("nf4_packed", ..) */
     NF4S_ERR_MISALIGNED = 4,         /* pointer alignment a kernel requires */
     NF4S_ERR_UNSUPPORTED_SHAPE = 5,  /* shape outside what a kernel supports */
-    NF4S_ERR_HIP = 6                 /* HIP runtime or launch error */
+    NF4S_ERR_HIP = 6,                /* HIP runtime or launch error */
+    NF4S_ERR_IO = 7,                 /* error.rs:7-9   ShardEngineError::Io */
+    NF4S_ERR_JSON = 8,               /* error.rs:11-13 ShardEngineError::Json */
+    NF4S_ERR_LAYER_NOT_FOUND = 9,    /* error.rs:15-17 ShardEngineError::LayerNotFound */
+    NF4S_ERR_PARAM_NOT_FOUND = 10,   /* error.rs:19-21 ShardEngineError::ParamNotFound */
+    NF4S_ERR_MALFORMED_INDEX = 11    /* error.rs:23-25 MalformedIndex (index entries) */
 };
 
 /*
@@ -171,6 +176,58 @@ int32_t nf4s_dbuf_release(nf4s_dbuf *d, const void *dev_ptr, void *compute_strea
 
 /* hipStreamWaitEvent on a ready event returned by nf4s_dbuf_advance. */
 int32_t nf4s_stream_wait_event(void *stream, void *event);
+
+/* ---------------------------------------------------------------------------
+ * Shard loader: the reference's on-disk NF4 format (shard_index.json +
+ * layer_registry.json + safetensors shards; shard_engine/src/index.rs:7-34,
+ * shard_engine/python/pipeline/writer.py:29-48,72-132), files mmap'd, NF4
+ * dequantized on the device.  A loader is used from one stream at a time
+ * (the reference's ShardLoader takes &mut self, loader.rs:36-40).
+ * ------------------------------------------------------------------------- */
+typedef struct nf4s_loader nf4s_loader;
+
+typedef struct nf4s_param_info {
+    int64_t shape[8];
+    int32_t ndim;
+    int32_t precision;     /* 0 fp16, 1 nf4, 2 nf4 with double-quant absmax */
+    int64_t numel;
+    int64_t byte_length;   /* TensorInfo.byte_length (packed bytes for nf4) */
+    int64_t absmax_len;    /* fp32 absmax entries, or double-quant codes */
+    int64_t scale_len;     /* double-quant fp32 scales */
+    int32_t block_size;
+    int32_t dq_group;
+    int64_t out_elems;     /* f16 elements load_param yields (2 * packed bytes for nf4) */
+    char precision_str[16];/* TensorInfo.precision ("nf4", "fp16", ...), NUL-terminated */
+    char dtype_str[16];    /* TensorInfo.dtype */
+} nf4s_param_info;
+
+/* ShardLoader::new (shard_engine/src/loader.rs:44-50): reads
+ * shard_index.json and layer_registry.json (index.rs:279-295). */
+int32_t nf4s_loader_open(const char *model_dir, nf4s_loader **out);
+int32_t nf4s_loader_close(nf4s_loader *l);
+
+/* IndexStore::tensor_info (index.rs:307-311) as a plain struct. */
+int32_t nf4s_loader_param_info(nf4s_loader *l, const char *name, nf4s_param_info *out);
+
+/* ShardLoader::load_layer (loader.rs:53-75): the layer's whole shard file
+ * (safetensors bytes), as a read-only mapping valid until nf4s_loader_close. */
+int32_t nf4s_loader_load_layer(nf4s_loader *l, uint32_t layer, const uint8_t **data,
+                               int64_t *len);
+
+/* ShardLoader::load_param (loader.rs:78-206) into a device f16 buffer of
+ * out_len elements: NF4 entries pass the reference's checks in its order
+ * (loader.rs:99-151) and are dequantized on the device with
+ * dequant_nf4_alloc semantics (2 * packed bytes elements, nf4.rs:98-107);
+ * fp16 entries are copied (loader.rs:179-198). */
+int32_t nf4s_loader_load_param_f16(nf4s_loader *l, const char *name, uint16_t *out,
+                                   int64_t out_len, void *stream);
+
+/* The raw NF4 payload of a parameter (packed bytes, fp32 absmax or uint8
+ * codes, fp32 scales) copied into caller device buffers, for a weight
+ * provider that keeps NF4 resident instead of widening it to f32
+ * (doublepass/src/shard_provider.rs:103-130). */
+int32_t nf4s_loader_load_param_nf4(nf4s_loader *l, const char *name, uint8_t *packed,
+                                   void *absmax_or_q, float *scale, void *stream);
 
 #ifdef __cplusplus
 }
