@@ -94,28 +94,70 @@ __device__ __forceinline__ uint32_t lookup16(const uint32_t tab[4], uint32_t sel
   return (b & mask) | (a & ~mask);
 }
 
-// Dequantize the 8 elements of one packed word w (byte k holds element 2k in
-// its high nibble and 2k+1 in its low nibble).  out[j] = elem 2j | elem 2j+1
-// << 16, i.e. natural element order in memory.
-__device__ __forceinline__ void lut_apply8(const Lut16 &t, uint32_t w, uint32_t out[4]) {
-  const uint32_t selE = (w >> 4) & 0x07070707u;
-  const uint32_t selO = w & 0x07070707u;
+// The lookup of one packed word w (byte k holds element 2k in its high nibble
+// and 2k+1 in its low nibble), split into stages so that a caller can spread
+// them between other instructions:
+//   word_select:  3-bit selectors and bit-3 masks of the even / odd nibbles
+//   word_even:    low and high result bytes of the 4 even elements
+//   word_odd:     low and high result bytes of the 4 odd elements
+//   word_merge:   out[j] = elem 2j | elem 2j+1 << 16 (natural element order)
+struct WordLookup {
+  uint32_t selE, selO, maskE, maskO;
+  uint32_t loE, hiE, loO, hiO;
+};
+
+__device__ __forceinline__ void word_select(uint32_t w, WordLookup &x) {
+  x.selE = (w >> 4) & 0x07070707u;
+  x.selO = w & 0x07070707u;
   const uint32_t mE = w & 0x80808080u;
-  const uint32_t maskE = (mE << 1) - (mE >> 7);
+  x.maskE = (mE << 1) - (mE >> 7);
   const uint32_t mO = w & 0x08080808u;
-  const uint32_t maskO = (mO << 5) - (mO >> 3);
-  const uint32_t loE = lookup16(t.lo, selE, maskE);
-  const uint32_t hiE = lookup16(t.hi, selE, maskE);
-  const uint32_t loO = lookup16(t.lo, selO, maskO);
-  const uint32_t hiO = lookup16(t.hi, selO, maskO);
-  const uint32_t e01 = perm(hiE, loE, 0x05010400u);  // elem0, elem2
-  const uint32_t e23 = perm(hiE, loE, 0x07030602u);  // elem4, elem6
-  const uint32_t o01 = perm(hiO, loO, 0x05010400u);  // elem1, elem3
-  const uint32_t o23 = perm(hiO, loO, 0x07030602u);  // elem5, elem7
+  x.maskO = (mO << 5) - (mO >> 3);
+}
+
+__device__ __forceinline__ void word_even(const Lut16 &t, WordLookup &x) {
+  x.loE = lookup16(t.lo, x.selE, x.maskE);
+  x.hiE = lookup16(t.hi, x.selE, x.maskE);
+}
+
+__device__ __forceinline__ void word_odd(const Lut16 &t, WordLookup &x) {
+  x.loO = lookup16(t.lo, x.selO, x.maskO);
+  x.hiO = lookup16(t.hi, x.selO, x.maskO);
+}
+
+__device__ __forceinline__ void word_merge(const WordLookup &x, uint32_t out[4]) {
+  const uint32_t e01 = perm(x.hiE, x.loE, 0x05010400u);  // elem0, elem2
+  const uint32_t e23 = perm(x.hiE, x.loE, 0x07030602u);  // elem4, elem6
+  const uint32_t o01 = perm(x.hiO, x.loO, 0x05010400u);  // elem1, elem3
+  const uint32_t o23 = perm(x.hiO, x.loO, 0x07030602u);  // elem5, elem7
   out[0] = perm(o01, e01, 0x05040100u);
   out[1] = perm(o01, e01, 0x07060302u);
   out[2] = perm(o23, e23, 0x05040100u);
   out[3] = perm(o23, e23, 0x07060302u);
+}
+
+// Dequantize the 8 elements of one packed word w; out[j] = elem 2j |
+// elem 2j+1 << 16, i.e. natural element order in memory.
+__device__ __forceinline__ void lut_apply8(const Lut16 &t, uint32_t w, uint32_t out[4]) {
+  WordLookup x;
+  word_select(w, x);
+  word_even(t, x);
+  word_odd(t, x);
+  word_merge(x, out);
+}
+
+// The product table built in 4 quarters (entries 4q..4q+3 each), for callers
+// that interleave it with other work.
+template <bool kF16>
+__device__ __forceinline__ void make_lut_quarter(float absmax, int q, Lut16 &t) {
+  const float p0 = fp32_rounded(code_value(4 * q) * absmax);
+  const float p1 = fp32_rounded(code_value(4 * q + 1) * absmax);
+  const float p2 = fp32_rounded(code_value(4 * q + 2) * absmax);
+  const float p3 = fp32_rounded(code_value(4 * q + 3) * absmax);
+  const uint32_t d0 = kF16 ? pack_f16x2(p0, p1) : pack_bf16x2(p0, p1);
+  const uint32_t d1 = kF16 ? pack_f16x2(p2, p3) : pack_bf16x2(p2, p3);
+  t.lo[q] = perm(d1, d0, 0x06040200u);
+  t.hi[q] = perm(d1, d0, 0x07050301u);
 }
 
 // Per-block absmax, fp32 or double-quantized: (float)q * scale[b >> shift]

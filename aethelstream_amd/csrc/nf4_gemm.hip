@@ -67,7 +67,6 @@ __device__ __forceinline__ float absmax_at(const AbsmaxRef &a, int64_t blk) {
 // consecutive k of one block; writes 4 swizzled 16-B units of its row.
 template <bool kDQ>
 struct FwdProducer {
-  static constexpr int kDsWritesPerWord = 1;
   const uint8_t *ptr;   // packed bytes of (row, half) at step 0
   int64_t am_idx;       // absmax block index at step 0
   int row, h;
@@ -83,21 +82,27 @@ struct FwdProducer {
     w = *reinterpret_cast<const u32x4 *>(ptr + step * 32);
     a = absmax_at<kDQ>(g.am, am_idx + step);
   }
-  __device__ __forceinline__ Lut16 table(float a) const { return make_lut<false>(a); }
-  // Dequantizes packed word k (8 elements) into LDS.
-  __device__ __forceinline__ void put(u32x4 *lds, const Lut16 &lut, uint32_t word, int k) const {
-    uint32_t o[4];
-    lut_apply8(lut, word, o);
+  // The absmax the product table is built from.
+  __device__ __forceinline__ float table_absmax(float a) const { return a; }
+  // Writes the 8 dequantized elements of packed word k (out[j] = elements
+  // 2j, 2j+1) in `part` of kStoreParts.
+  static constexpr int kStoreParts = 1;
+  __device__ __forceinline__ void store(u32x4 *lds, const uint32_t out[4], int k, int part) const {
+    (void)part;
     u32x4 v;
-    v.x = o[0]; v.y = o[1]; v.z = o[2]; v.w = o[3];
+    v.x = out[0]; v.y = out[1]; v.z = out[2]; v.w = out[3];
     lds[lds_unit(row, 4 * h + k)] = v;
   }
+  // Whole-tile store (prologue).
   __device__ __forceinline__ void store(u32x4 *lds, const u32x4 &w, float a) const {
-    const Lut16 lut = table(a);
-    put(lds, lut, w.x, 0);
-    put(lds, lut, w.y, 1);
-    put(lds, lut, w.z, 2);
-    put(lds, lut, w.w, 3);
+    const Lut16 lut = make_lut<false>(table_absmax(a));
+    const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      uint32_t o[4];
+      lut_apply8(lut, words[k], o);
+      store(lds, o, k, 0);
+    }
   }
 };
 
@@ -108,7 +113,6 @@ struct FwdProducer {
 // each element is written as one 16-bit value.
 template <bool kDQ>
 struct DgradProducer {
-  static constexpr int kDsWritesPerWord = 8;
   const uint8_t *ptr;
   int64_t am_idx;
   int r, q;
@@ -128,27 +132,33 @@ struct DgradProducer {
     w = *reinterpret_cast<const u32x4 *>(ptr + step * 64 * (g.wk >> 1));
     a = absmax_at<kDQ>(g.am, am_idx + step * 64 * (g.wk >> 6));
   }
-  __device__ __forceinline__ Lut16 table(float a) const {
-    // Columns beyond k read column 0's bytes and are zeroed via the absmax.
-    return make_lut<false>(__builtin_bit_cast(float, __builtin_bit_cast(uint32_t, a) & valid_mask));
+  // Columns beyond k read column 0's bytes and are zeroed via the absmax.
+  __device__ __forceinline__ float table_absmax(float a) const {
+    return __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, a) & valid_mask);
   }
-  __device__ __forceinline__ void put(u32x4 *lds, const Lut16 &lut, uint32_t word, int k) const {
-    uint32_t o[4];
-    lut_apply8(lut, word, o);
+  // Writes the 8 elements of packed word k as 16-bit values down 8 LDS rows
+  // (output columns); part p of 4 writes elements 2p and 2p+1.
+  static constexpr int kStoreParts = 4;
+  __device__ __forceinline__ void store(u32x4 *lds, const uint32_t out[4], int k, int part) const {
     uint16_t *l16 = reinterpret_cast<uint16_t *>(lds);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int jj = 0; jj < 2; ++jj) {
+      const int j = 2 * part + jj;
       const int col = 32 * q + 8 * k + j;  // LDS row (output column)
-      const uint16_t v = (uint16_t)((j & 1) ? (o[j >> 1] >> 16) : (o[j >> 1] & 0xffffu));
+      const uint16_t v = (uint16_t)((j & 1) ? (out[j >> 1] >> 16) : (out[j >> 1] & 0xffffu));
       l16[lds_unit(col, r >> 3) * 8 + (r & 7)] = v;
     }
   }
   __device__ __forceinline__ void store(u32x4 *lds, const u32x4 &w, float a) const {
-    const Lut16 lut = table(a);
-    put(lds, lut, w.x, 0);
-    put(lds, lut, w.y, 1);
-    put(lds, lut, w.z, 2);
-    put(lds, lut, w.w, 3);
+    const Lut16 lut = make_lut<false>(table_absmax(a));
+    const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      uint32_t o[4];
+      lut_apply8(lut, words[k], o);
+#pragma unroll
+      for (int p = 0; p < 4; ++p) store(lds, o, k, p);
+    }
   }
 };
 
@@ -179,18 +189,18 @@ __shared__ u32x4 g_lds_b1[1024];
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
-// One 64-deep reduction step.  The activation tile of this step is in
-// LDS (this wave's part of Acur), the weight tile in Bcur.  Alongside the 64
-// MFMAs it
+// One 64-deep reduction step: 4 sub-steps of 16 MFMAs over the activation
+// tile in Acur (this wave's rows) and the weight tile in Bcur.  Alongside it
 //   * starts the direct-to-LDS loads of the next step's activation tile into
 //     Anext (16 instructions of 1 KB, 8 full 128-B rows each),
 //   * loads the packed weight bytes of step t+2 (wn_, an_),
-//   * dequantizes step t+1's weights (wc, ac) into Bnext, one packed word
-//     (8 elements) per sub-step, the product table in sub-step 0.
-// Each sub-step is its own scheduling region (sched_barrier fences) in which
-// sched_group_barrier places VALU, LDS and memory instructions between the
-// MFMAs: a wave issues in order, so other work only overlaps the matrix pipe
-// when it sits between MFMAs in the instruction stream.
+//   * dequantizes step t+1's weights (wc, ac) into Bnext: product table in
+//     sub-step 0, packed word s in sub-step s,
+//   * prefetches the next sub-step's A and B fragments.
+// A wave issues in order, so other work only overlaps the matrix pipe when
+// it sits between MFMAs in the instruction stream: every MFMA is followed by
+// one small piece of that work (a few VALU ops, two LDS reads or one DMA),
+// and sched_barrier fences keep that order.
 template <class Producer>
 __device__ __forceinline__ void gemm_step(const GemmArgs &g, const Producer &prod,
                                           floatx16 (&acc)[4][4], const u32x4 *__restrict__ Acur,
@@ -203,8 +213,10 @@ __device__ __forceinline__ void gemm_step(const GemmArgs &g, const Producer &pro
   const int64_t t1 = (t + 1 < nsteps) ? t + 1 : nsteps - 1;
   const int64_t t2 = (t + 2 < nsteps) ? t + 2 : nsteps - 1;
   const uint32_t words[4] = {wc.x, wc.y, wc.z, wc.w};
+  const float ta = prod.table_absmax(ac);
   Lut16 lut;
-  // Fragments of sub-step s: A (4 m-tiles) and B (4 n-tiles), double-buffered.
+  WordLookup wl;
+  uint32_t wout[2][4];
   u32x4 a[2][4], b[2][4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -213,45 +225,51 @@ __device__ __forceinline__ void gemm_step(const GemmArgs &g, const Producer &pro
     b[0][i] = Bcur[lds_unit(row, grp)];
   }
   prod.load(g, t2, wn_, an_);
+  __builtin_amdgcn_sched_barrier(0);
+  // Slot plan after MFMA i of sub-step s:
+  //   i 0-3   (s < 3) two fragment reads of sub-step s+1
+  //   i 4-7   one activation DMA (4s + i - 4); for s = 1 also stores of word 0
+  //           when the producer writes a word in parts
+  //   i 8-11  s = 0: product-table quarters; s > 0: lookup stages of word s
+  //   i 12-15 s = 0: lookup stages of word 0; s > 0: parts of word s's store
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
-    if (s == 0) lut = prod.table(ac);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const char *src = abase + t1 * (kStep * 2) + aoff[4 * s + i];
-      __builtin_amdgcn_global_load_lds(src, (lds_void_t *)(Anext_wave + (4 * s + i) * 64), 16, 0,
-                                       0);
-    }
-    if (s < 3) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = 32 * i + jl;
-        a[(s + 1) & 1][i] = Acur[lds_unit(row, 2 * (s + 1) + grp)];
-        b[(s + 1) & 1][i] = Bcur[lds_unit(row, 2 * (s + 1) + grp)];
-      }
-    }
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-      for (int nt = 0; nt < 4; ++nt)
-        acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-            __builtin_bit_cast(bf16x8, a[s & 1][mt]), __builtin_bit_cast(bf16x8, b[s & 1][nt]),
-            acc[mt][nt], 0, 0, 0);
-    prod.put(Bnext, lut, words[s], s);
-
-    // 16 MFMAs; the dequant's VALU (table + one word, ~28-60 ops) 4 per MFMA;
-    // the next sub-step's 8 fragment reads early; 4 DMA loads; LDS writes late.
-    if (s == 0) __builtin_amdgcn_sched_group_barrier(kSgVmem, 2, 0);
+    const int n = (s + 1) & 1;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      __builtin_amdgcn_sched_group_barrier(kSgMfma, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(kSgValu, 4, 0);
-      if (s < 3 && i < 8) __builtin_amdgcn_sched_group_barrier(kSgDsRead, 1, 0);
-      if (i >= 2 && i < 6) __builtin_amdgcn_sched_group_barrier(kSgVmem, 1, 0);
-      if (i >= 8 && i < 8 + Producer::kDsWritesPerWord)
-        __builtin_amdgcn_sched_group_barrier(kSgDsWrite, 1, 0);
+      const int mt = i >> 2, nt = i & 3;
+      acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+          __builtin_bit_cast(bf16x8, a[s & 1][mt]), __builtin_bit_cast(bf16x8, b[s & 1][nt]),
+          acc[mt][nt], 0, 0, 0);
+      if (s < 3 && i < 4) {
+        const int u = 2 * (s + 1) + grp;
+        if (i < 2) {
+          a[n][2 * i] = Acur[lds_unit(64 * i + jl, u)];
+          a[n][2 * i + 1] = Acur[lds_unit(64 * i + 32 + jl, u)];
+        } else {
+          b[n][2 * (i - 2)] = Bcur[lds_unit(64 * (i - 2) + jl, u)];
+          b[n][2 * (i - 2) + 1] = Bcur[lds_unit(64 * (i - 2) + 32 + jl, u)];
+        }
+      }
+      if (i >= 4 && i < 8) {
+        const int d = 4 * s + (i - 4);
+        __builtin_amdgcn_global_load_lds(abase + t1 * (kStep * 2) + aoff[d],
+                                         (lds_void_t *)(Anext_wave + d * 64), 16, 0, 0);
+        if (Producer::kStoreParts > 1 && s == 1) prod.store(Bnext, wout[0], 0, i - 4);
+      }
+      const int stage = (s == 0) ? i - 12 : i - 8;  // lookup stage of word s
+      if (s == 0 && i >= 8 && i < 12) make_lut_quarter<false>(ta, i - 8, lut);
+      if (stage == 0) word_select(words[s], wl);
+      if (stage == 1) word_even(lut, wl);
+      if (stage == 2) word_odd(lut, wl);
+      if (stage == 3) {
+        word_merge(wl, wout[s & 1]);
+        if (Producer::kStoreParts == 1) prod.store(Bnext, wout[s & 1], s, 0);
+      }
+      if (Producer::kStoreParts > 1 && s > 0 && i >= 12)
+        prod.store(Bnext, wout[s & 1], s, i - 12);
+      __builtin_amdgcn_sched_barrier(0);
     }
-    __builtin_amdgcn_sched_barrier(0);
   }
 }
 
