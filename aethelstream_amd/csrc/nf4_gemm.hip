@@ -8,9 +8,10 @@
 // Workgroup = 4 waves, tile = 512 rows of the activation x 128 output columns.
 // Each wave owns 128 rows and keeps a 128x128 fp32 accumulator (16 MFMA
 // tiles of 32x32, 256 registers).  Per 64-deep reduction step:
-//   * each wave loads its activation fragments straight from global memory
-//     into registers (no LDS round trip, no sharing needed: rows are private
-//     to the wave); the next step's fragments are in flight during this one;
+//   * each wave moves its next activation tile (128 rows x 64 bf16) from
+//     global memory into its own LDS buffer with direct-to-LDS loads, each
+//     instruction one coalesced 1 KB run of 8 whole rows; the MFMA fragments
+//     are then read from LDS;
 //   * the workgroup dequantizes the step's 128x64 weight tile ONCE into LDS
 //     as bf16 (16-entry per-block product table in registers, v_perm_b32
 //     lookups), so the dequant cost is amortised over 512 activation rows;
