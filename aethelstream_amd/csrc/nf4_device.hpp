@@ -106,13 +106,17 @@ struct WordLookup {
   uint32_t loE, hiE, loO, hiO;
 };
 
+// v_perm_b32 selector values 8, 9, 10 and 11 replicate the top bit of byte
+// 1, 3, 5 and 7 of {hi4:lo4} into a whole byte.  With hi4 = v and
+// lo4 = v << 8, bytes 1, 3, 5, 7 are bytes 0, 2, 1, 3 of v, so kSignBytes
+// turns bit 7 of every byte of v into a 0x00 / 0xff byte mask.
+constexpr uint32_t kSignBytes = 0x0B090A08u;
+
 __device__ __forceinline__ void word_select(uint32_t w, WordLookup &x) {
   x.selE = (w >> 4) & 0x07070707u;
   x.selO = w & 0x07070707u;
-  const uint32_t mE = w & 0x80808080u;
-  x.maskE = (mE << 1) - (mE >> 7);
-  const uint32_t mO = w & 0x08080808u;
-  x.maskO = (mO << 5) - (mO >> 3);
+  x.maskE = perm(w, w << 8, kSignBytes);          // bit 3 of each high nibble
+  x.maskO = perm(w << 4, w << 12, kSignBytes);    // bit 3 of each low nibble
 }
 
 __device__ __forceinline__ void word_even(const Lut16 &t, WordLookup &x) {
@@ -125,15 +129,24 @@ __device__ __forceinline__ void word_odd(const Lut16 &t, WordLookup &x) {
   x.hiO = lookup16(t.hi, x.selO, x.maskO);
 }
 
+// First half of the merge: whole 16-bit elements, pairs in the order
+//   pairs[0] = elem0 | elem2 << 16    pairs[1] = elem1 | elem3 << 16
+//   pairs[2] = elem4 | elem6 << 16    pairs[3] = elem5 | elem7 << 16
+// so element j is half (j >> 1) & 1 of pairs[(j & 1) + 2 * (j >> 2)].
+__device__ __forceinline__ void word_pairs(const WordLookup &x, uint32_t pairs[4]) {
+  pairs[0] = perm(x.hiE, x.loE, 0x05010400u);
+  pairs[1] = perm(x.hiO, x.loO, 0x05010400u);
+  pairs[2] = perm(x.hiE, x.loE, 0x07030602u);
+  pairs[3] = perm(x.hiO, x.loO, 0x07030602u);
+}
+
 __device__ __forceinline__ void word_merge(const WordLookup &x, uint32_t out[4]) {
-  const uint32_t e01 = perm(x.hiE, x.loE, 0x05010400u);  // elem0, elem2
-  const uint32_t e23 = perm(x.hiE, x.loE, 0x07030602u);  // elem4, elem6
-  const uint32_t o01 = perm(x.hiO, x.loO, 0x05010400u);  // elem1, elem3
-  const uint32_t o23 = perm(x.hiO, x.loO, 0x07030602u);  // elem5, elem7
-  out[0] = perm(o01, e01, 0x05040100u);
-  out[1] = perm(o01, e01, 0x07060302u);
-  out[2] = perm(o23, e23, 0x05040100u);
-  out[3] = perm(o23, e23, 0x07060302u);
+  uint32_t p[4];
+  word_pairs(x, p);
+  out[0] = perm(p[1], p[0], 0x05040100u);
+  out[1] = perm(p[1], p[0], 0x07060302u);
+  out[2] = perm(p[3], p[2], 0x05040100u);
+  out[3] = perm(p[3], p[2], 0x07060302u);
 }
 
 // Dequantize the 8 elements of one packed word w; out[j] = elem 2j |

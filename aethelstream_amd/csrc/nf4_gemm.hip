@@ -55,6 +55,25 @@ struct GemmArgs {
 // fragment spread over all banks.
 __device__ __forceinline__ int lds_unit(int row, int u) { return row * 8 + (u ^ (row & 7)); }
 
+// Weight tile: the same swizzle XOR 2 * ((row / 32) % 4).  The extra term is
+// constant over the 32 rows of one fragment read, so reads stay spread over
+// the banks, and it spreads the dgrad producer's 16-bit stores (whose lanes
+// cover output columns 32 apart) over all banks too.
+__device__ __forceinline__ int lds_unit_b(int row, int u) {
+  return row * 8 + (u ^ (row & 7) ^ ((row >> 4) & 6));
+}
+
+// Lookup of packed word w with product table t, finished by the producer's
+// merge.
+template <class Producer>
+__device__ __forceinline__ void dequant_word(const Lut16 &t, uint32_t w, uint32_t out[4]) {
+  WordLookup x;
+  word_select(w, x);
+  word_even(t, x);
+  word_odd(t, x);
+  Producer::merge(x, out);
+}
+
 // Absmax of block `blk`: fp32, or the double-quant code times its group scale.
 // A template flag rather than a runtime test keeps the GEMM step one basic
 // block (one scheduling region).
@@ -85,14 +104,18 @@ struct FwdProducer {
   }
   // The absmax the product table is built from.
   __device__ __forceinline__ float table_absmax(float a) const { return a; }
-  // Writes the 8 dequantized elements of packed word k (out[j] = elements
-  // 2j, 2j+1) in `part` of kStoreParts.
+  // The 8 elements of a word in natural order: out[j] = elements 2j, 2j+1.
+  static __device__ __forceinline__ void merge(const WordLookup &x, uint32_t out[4]) {
+    word_merge(x, out);
+  }
+  // Writes the 8 dequantized elements of packed word k in `part` of
+  // kStoreParts.
   static constexpr int kStoreParts = 1;
   __device__ __forceinline__ void store(u32x4 *lds, const uint32_t out[4], int k, int part) const {
     (void)part;
     u32x4 v;
     v.x = out[0]; v.y = out[1]; v.z = out[2]; v.w = out[3];
-    lds[lds_unit(row, 4 * h + k)] = v;
+    lds[lds_unit_b(row, 4 * h + k)] = v;
   }
   // Whole-tile store (prologue).
   __device__ __forceinline__ void store(u32x4 *lds, const u32x4 &w, float a) const {
@@ -101,7 +124,7 @@ struct FwdProducer {
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       uint32_t o[4];
-      lut_apply8(lut, words[k], o);
+      dequant_word<FwdProducer>(lut, words[k], o);
       store(lds, o, k, 0);
     }
   }
@@ -137,6 +160,11 @@ struct DgradProducer {
   __device__ __forceinline__ float table_absmax(float a) const {
     return __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, a) & valid_mask);
   }
+  // Elements are stored one by one, so the pairs of the first merge half
+  // suffice: element j is half (j >> 1) & 1 of out[(j & 1) + 2 * (j >> 2)].
+  static __device__ __forceinline__ void merge(const WordLookup &x, uint32_t out[4]) {
+    word_pairs(x, out);
+  }
   // Writes the 8 elements of packed word k as 16-bit values down 8 LDS rows
   // (output columns); part p of 4 writes elements 2p and 2p+1.
   static constexpr int kStoreParts = 4;
@@ -146,8 +174,9 @@ struct DgradProducer {
     for (int jj = 0; jj < 2; ++jj) {
       const int j = 2 * part + jj;
       const int col = 32 * q + 8 * k + j;  // LDS row (output column)
-      const uint16_t v = (uint16_t)((j & 1) ? (out[j >> 1] >> 16) : (out[j >> 1] & 0xffffu));
-      l16[lds_unit(col, r >> 3) * 8 + (r & 7)] = v;
+      const uint32_t pr = out[(j & 1) + 2 * (j >> 2)];
+      const uint16_t v = (uint16_t)(((j >> 1) & 1) ? (pr >> 16) : (pr & 0xffffu));
+      l16[lds_unit_b(col, r >> 3) * 8 + (r & 7)] = v;
     }
   }
   __device__ __forceinline__ void store(u32x4 *lds, const u32x4 &w, float a) const {
@@ -156,7 +185,7 @@ struct DgradProducer {
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       uint32_t o[4];
-      lut_apply8(lut, words[k], o);
+      dequant_word<DgradProducer>(lut, words[k], o);
 #pragma unroll
       for (int p = 0; p < 4; ++p) store(lds, o, k, p);
     }
@@ -177,10 +206,6 @@ __device__ __forceinline__ void map_tile(int tiles_m, int tiles_o, int &tm, int 
   to = L - tm * tiles_o;
 }
 
-// sched_group_barrier masks
-constexpr int kSgMfma = 0x008, kSgValu = 0x002, kSgVmem = 0x010;
-constexpr int kSgDsRead = 0x100, kSgDsWrite = 0x200;
-
 // LDS: two activation buffers (per wave 128 rows x 128 B = 16 KB; 4 waves =
 // 64 KB each) and two weight tiles (16 KB each): 160 KB, the gfx950 maximum.
 __shared__ u32x4 g_lds_a0[4 * 1024];
@@ -189,6 +214,9 @@ __shared__ u32x4 g_lds_b0[1024];
 __shared__ u32x4 g_lds_b1[1024];
 
 typedef __attribute__((address_space(3))) void lds_void_t;
+
+// Word 3 of a raw (stride 0) gfx9 buffer resource: 32-bit data format.
+constexpr int kBufferFlags = 0x00020000;
 
 // One 64-deep reduction step: 4 sub-steps of 16 MFMAs over the activation
 // tile in Acur (this wave's rows) and the weight tile in Bcur.  Alongside it
@@ -208,7 +236,7 @@ __device__ __forceinline__ void gemm_step(const GemmArgs &g, const Producer &pro
                                           u32x4 *__restrict__ Anext_wave,
                                           const u32x4 *__restrict__ Bcur,
                                           u32x4 *__restrict__ Bnext,
-                                          const char *abase, const uint32_t (&aoff)[16],
+                                          __amdgpu_buffer_rsrc_t arsrc, const uint32_t (&aoff)[16],
                                           const u32x4 &wc, float ac, u32x4 &wn_, float &an_,
                                           int64_t t, int64_t nsteps, int jl, int grp) {
   const int64_t t1 = (t + 1 < nsteps) ? t + 1 : nsteps - 1;
@@ -223,7 +251,7 @@ __device__ __forceinline__ void gemm_step(const GemmArgs &g, const Producer &pro
   for (int i = 0; i < 4; ++i) {
     const int row = 32 * i + jl;
     a[0][i] = Acur[lds_unit(row, grp)];
-    b[0][i] = Bcur[lds_unit(row, grp)];
+    b[0][i] = Bcur[lds_unit_b(row, grp)];
   }
   prod.load(g, t2, wn_, an_);
   __builtin_amdgcn_sched_barrier(0);
@@ -248,14 +276,14 @@ __device__ __forceinline__ void gemm_step(const GemmArgs &g, const Producer &pro
           a[n][2 * i] = Acur[lds_unit(64 * i + jl, u)];
           a[n][2 * i + 1] = Acur[lds_unit(64 * i + 32 + jl, u)];
         } else {
-          b[n][2 * (i - 2)] = Bcur[lds_unit(64 * (i - 2) + jl, u)];
-          b[n][2 * (i - 2) + 1] = Bcur[lds_unit(64 * (i - 2) + 32 + jl, u)];
+          b[n][2 * (i - 2)] = Bcur[lds_unit_b(64 * (i - 2) + jl, u)];
+          b[n][2 * (i - 2) + 1] = Bcur[lds_unit_b(64 * (i - 2) + 32 + jl, u)];
         }
       }
       if (i >= 4 && i < 8) {
         const int d = 4 * s + (i - 4);
-        __builtin_amdgcn_global_load_lds(abase + t1 * (kStep * 2) + aoff[d],
-                                         (lds_void_t *)(Anext_wave + d * 64), 16, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(arsrc, (lds_void_t *)(Anext_wave + d * 64), 16,
+                                                 (int)aoff[d], (int)(t1 * (kStep * 2)), 0, 0);
         if (Producer::kStoreParts > 1 && s == 1) prod.store(Bnext, wout[0], 0, i - 4);
       }
       const int stage = (s == 0) ? i - 12 : i - 8;  // lookup stage of word s
@@ -264,7 +292,7 @@ __device__ __forceinline__ void gemm_step(const GemmArgs &g, const Producer &pro
       if (stage == 1) word_even(lut, wl);
       if (stage == 2) word_odd(lut, wl);
       if (stage == 3) {
-        word_merge(wl, wout[s & 1]);
+        Producer::merge(wl, wout[s & 1]);
         if (Producer::kStoreParts == 1) prod.store(Bnext, wout[s & 1], s, 0);
       }
       if (Producer::kStoreParts > 1 && s > 0 && i >= 12)
@@ -290,7 +318,10 @@ __global__ void __launch_bounds__(kGemmThreads, 1) nf4_gemm_kernel(const GemmArg
   // wave's 128-row tile as 1 KB, lane p at LDS unit 64i + p, i.e. row
   // 8i + p/8, physical unit p%8, which holds logical unit (p%8) ^ (row%8)
   // (the swizzle of lds_unit).  aoff[i] is lane p's byte offset from the
-  // wave's first (clamped) row at k = 0; rows beyond M are clamped.
+  // wave's first (clamped) row at k = 0; rows beyond M are clamped.  The
+  // loads go through a buffer resource based at that row, with the step's
+  // k offset in a scalar register, so the loop spends no vector ALU work on
+  // their addresses (check_gemm bounds every offset below 2^31).
   const int64_t mb = (m0 < g.M) ? m0 : g.M - 1;
   const char *abase = reinterpret_cast<const char *>(g.a + mb * g.lda);
   // Rows available to this wave from mb (at least 1, at most 128).
@@ -298,6 +329,8 @@ __global__ void __launch_bounds__(kGemmThreads, 1) nf4_gemm_kernel(const GemmArg
   const int32_t avail = (int32_t)(avail64 > 128 ? 128 : avail64);
   const uint32_t lda2 = (uint32_t)(g.lda * 2);
   const int32_t skip = (int32_t)(m0 - mb);  // > 0 only when the whole wave is past M
+  const __amdgpu_buffer_rsrc_t arsrc =
+      __builtin_amdgcn_make_buffer_rsrc((void *)abase, 0, 0x7fffffff, kBufferFlags);
   uint32_t aoff[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
@@ -326,7 +359,8 @@ __global__ void __launch_bounds__(kGemmThreads, 1) nf4_gemm_kernel(const GemmArg
   // (dequantized into b0), packed weights of step 1 in registers.
 #pragma unroll
   for (int i = 0; i < 16; ++i)
-    __builtin_amdgcn_global_load_lds(abase + aoff[i], (lds_void_t *)(a0w + i * 64), 16, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(arsrc, (lds_void_t *)(a0w + i * 64), 16, (int)aoff[i],
+                                             0, 0, 0);
   {
     u32x4 w0;
     float s0;
@@ -346,7 +380,7 @@ __global__ void __launch_bounds__(kGemmThreads, 1) nf4_gemm_kernel(const GemmArg
   for (int64_t t = 0; t < nsteps; ++t) {
     const bool odd = (t & 1) != 0;
     gemm_step<Producer>(g, prod, acc, odd ? a1w : a0w, odd ? a0w : a1w, odd ? g_lds_b1 : g_lds_b0,
-                        odd ? g_lds_b0 : g_lds_b1, abase, aoff, wc, ac, wn, an, t, nsteps, jl,
+                        odd ? g_lds_b0 : g_lds_b1, arsrc, aoff, wc, ac, wn, an, t, nsteps, jl,
                         grp);
     // Next step's activation tile (direct-to-LDS) and weight tile complete.
     __builtin_amdgcn_s_waitcnt(0);
@@ -410,6 +444,14 @@ static int32_t check_gemm(const uint16_t *act, const nf4s_tensor *w, int64_t m, 
   return NF4S_OK;
 }
 
+// The activation loads address a wave's 128 rows with 32-bit offsets.
+static int32_t check_offsets(int64_t lda) {
+  if (lda > (int64_t)1 << 22)
+    return fail(NF4S_ERR_UNSUPPORTED_SHAPE, "activation row of %lld elements is too long",
+                (long long)lda);
+  return NF4S_OK;
+}
+
 template <class Producer>
 static int32_t launch_gemm(const GemmArgs &g, hipStream_t s, const char *name) {
   const int64_t T = (int64_t)g.tiles_m * g.tiles_o;
@@ -428,6 +470,7 @@ extern "C" {
 int32_t nf4s_gemm_fwd(const uint16_t *x, const nf4s_tensor *w, int64_t m, int64_t n, int64_t k,
                       uint16_t *y, void *stream) {
   int32_t rc = check_gemm(x, w, m, n, k, y);
+  if (rc == NF4S_OK) rc = check_offsets(k);
   if (rc != NF4S_OK) return rc;
   if (m == 0) return NF4S_OK;
   GemmArgs g{};
@@ -452,6 +495,7 @@ int32_t nf4s_gemm_fwd(const uint16_t *x, const nf4s_tensor *w, int64_t m, int64_
 int32_t nf4s_gemm_dgrad(const uint16_t *dy, const nf4s_tensor *w, int64_t m, int64_t n,
                         int64_t k, uint16_t *dx, void *stream) {
   int32_t rc = check_gemm(dy, w, m, n, k, dx);
+  if (rc == NF4S_OK) rc = check_offsets(n);
   if (rc != NF4S_OK) return rc;
   if (n % 64 != 0)
     return fail(NF4S_ERR_UNSUPPORTED_SHAPE, "dgrad needs n %% 64 == 0, got %lld", (long long)n);
