@@ -74,13 +74,31 @@ __device__ __forceinline__ void dequant_word(const Lut16 &t, uint32_t w, uint32_
   Producer::merge(x, out);
 }
 
-// Absmax of block `blk`: fp32, or the double-quant code times its group scale.
-// A template flag rather than a runtime test keeps the GEMM step one basic
-// block (one scheduling region).
+// Absmax of block `blk`: fp32, or the double-quant code times its group
+// scale.  It is loaded as raw words and decoded a step later, so that the
+// loads' latency never stalls the wave.  A template flag rather than a
+// runtime test keeps the GEMM step one basic block (one scheduling region).
+struct AbsRaw {
+  float s;     // fp32 absmax, or the group scale
+  uint32_t q;  // double-quant code (0 without double-quant)
+};
+
 template <bool kDQ>
-__device__ __forceinline__ float absmax_at(const AbsmaxRef &a, int64_t blk) {
-  if (kDQ) return (float)a.q[blk] * a.scale[blk >> a.group_shift];
-  return a.absmax[blk];
+__device__ __forceinline__ AbsRaw absmax_load(const AbsmaxRef &a, int64_t blk) {
+  AbsRaw r;
+  if (kDQ) {
+    r.q = a.q[blk];
+    r.s = a.scale[blk >> a.group_shift];
+  } else {
+    r.q = 0;
+    r.s = a.absmax[blk];
+  }
+  return r;
+}
+
+template <bool kDQ>
+__device__ __forceinline__ float absmax_value(const AbsRaw &r) {
+  return kDQ ? (float)r.q * r.s : r.s;
 }
 
 // Forward producer: thread -> (row n_local = tid/2, half h = tid%2), 32
@@ -98,12 +116,14 @@ struct FwdProducer {
     ptr = g.packed + n * (g.wk >> 1) + 16 * h;
     am_idx = n * (g.wk >> 6);
   }
-  __device__ __forceinline__ void load(const GemmArgs &g, int64_t step, u32x4 &w, float &a) const {
+  __device__ __forceinline__ void load(const GemmArgs &g, int64_t step, u32x4 &w, AbsRaw &a) const {
     w = *reinterpret_cast<const u32x4 *>(ptr + step * 32);
-    a = absmax_at<kDQ>(g.am, am_idx + step);
+    a = absmax_load<kDQ>(g.am, am_idx + step);
   }
   // The absmax the product table is built from.
-  __device__ __forceinline__ float table_absmax(float a) const { return a; }
+  __device__ __forceinline__ float table_absmax(const AbsRaw &a) const {
+    return absmax_value<kDQ>(a);
+  }
   // The 8 elements of a word in natural order: out[j] = elements 2j, 2j+1.
   static __device__ __forceinline__ void merge(const WordLookup &x, uint32_t out[4]) {
     word_merge(x, out);
@@ -118,7 +138,7 @@ struct FwdProducer {
     lds[lds_unit_b(row, 4 * h + k)] = v;
   }
   // Whole-tile store (prologue).
-  __device__ __forceinline__ void store(u32x4 *lds, const u32x4 &w, float a) const {
+  __device__ __forceinline__ void store(u32x4 *lds, const u32x4 &w, const AbsRaw &a) const {
     const Lut16 lut = make_lut<false>(table_absmax(a));
     const uint32_t words[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
@@ -151,14 +171,14 @@ struct DgradProducer {
     ptr = g.packed + (int64_t)r * (g.wk >> 1) + (c >> 1);
     am_idx = (int64_t)r * (g.wk >> 6) + (c >> 6);
   }
-  __device__ __forceinline__ void load(const GemmArgs &g, int64_t step, u32x4 &w, float &a) const {
+  __device__ __forceinline__ void load(const GemmArgs &g, int64_t step, u32x4 &w, AbsRaw &a) const {
     // Step s covers W rows 64s .. 64s+63.
     w = *reinterpret_cast<const u32x4 *>(ptr + step * 64 * (g.wk >> 1));
-    a = absmax_at<kDQ>(g.am, am_idx + step * 64 * (g.wk >> 6));
+    a = absmax_load<kDQ>(g.am, am_idx + step * 64 * (g.wk >> 6));
   }
   // Columns beyond k read column 0's bytes and are zeroed via the absmax.
-  __device__ __forceinline__ float table_absmax(float a) const {
-    return __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, a) & valid_mask);
+  __device__ __forceinline__ float table_absmax(const AbsRaw &a) const {
+    return __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, absmax_value<kDQ>(a)) & valid_mask);
   }
   // Elements are stored one by one, so the pairs of the first merge half
   // suffice: element j is half (j >> 1) & 1 of out[(j & 1) + 2 * (j >> 2)].
@@ -179,7 +199,7 @@ struct DgradProducer {
       l16[lds_unit_b(col, r >> 3) * 8 + (r & 7)] = v;
     }
   }
-  __device__ __forceinline__ void store(u32x4 *lds, const u32x4 &w, float a) const {
+  __device__ __forceinline__ void store(u32x4 *lds, const u32x4 &w, const AbsRaw &a) const {
     const Lut16 lut = make_lut<false>(table_absmax(a));
     const uint32_t words[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
@@ -223,21 +243,37 @@ constexpr int kBufferFlags = 0x00020000;
 //   * starts the direct-to-LDS loads of the next step's activation tile into
 //     Anext (16 instructions of 1 KB, 8 full 128-B rows each),
 //   * loads the packed weight bytes of step t+2 (wn_, an_),
-//   * dequantizes step t+1's weights (wc, ac) into Bnext: product table in
-//     sub-step 0, packed word s in sub-step s,
+//   * dequantizes step t+1's weights (wc, ac) into Bnext,
 //   * prefetches the next sub-step's A and B fragments.
 // A wave issues in order, so other work only overlaps the matrix pipe when
 // it sits between MFMAs in the instruction stream: every MFMA is followed by
-// one small piece of that work (a few VALU ops, two LDS reads or one DMA),
-// and sched_barrier fences keep that order.
+// one small piece of that work (a few VALU ops, two LDS reads, a DMA), and
+// sched_barrier fences keep that order.
+//
+// The step ends at the workgroup barrier after MFMA 11 of sub-step 3; its
+// last 4 MFMAs (a[1][3] x b[1][0..3], operands already in registers) open
+// the NEXT call, after the barrier, each followed by one pair of fragment
+// reads of the new step's sub-step 0, so those reads' latency hides behind
+// matrix work.  The first call runs them on zero operands.
+//
+// Slot plan, after MFMA i of sub-step s (R = fragment-read pair for s+1,
+// D = activation DMA, L = product-table quarter, W = lookup stage of a
+// packed word, P = part of a word's 16-bit transposed store):
+//   s=0: i0-3 R + D0-3   i4-7 L0-3     i8-11 W(0)    i12-15 D4-7
+//   s=1: i0-3 R + D8-11  i4-7 W(1)     i8-11 P(0)    i12-15 D12-15
+//   s=2: i0-3 R          i4-7 W(2)     i8-11 P(1)
+//   s=3: i0-3 P(2)       i4-7 W(3)     i8-11 P(3)    -> barrier
+// The DMAs are all issued by the middle of the step, so they have landed
+// by the barrier.
 template <class Producer>
 __device__ __forceinline__ void gemm_step(const GemmArgs &g, const Producer &prod,
-                                          floatx16 (&acc)[4][4], const u32x4 *__restrict__ Acur,
+                                          floatx16 (&acc)[4][4], u32x4 (&a)[2][4],
+                                          u32x4 (&b)[2][4], const u32x4 *__restrict__ Acur,
                                           u32x4 *__restrict__ Anext_wave,
                                           const u32x4 *__restrict__ Bcur,
                                           u32x4 *__restrict__ Bnext,
                                           __amdgpu_buffer_rsrc_t arsrc, const uint32_t (&aoff)[16],
-                                          const u32x4 &wc, float ac, u32x4 &wn_, float &an_,
+                                          const u32x4 &wc, const AbsRaw &ac, u32x4 &wn_, AbsRaw &an_,
                                           int64_t t, int64_t nsteps, int jl, int grp) {
   const int64_t t1 = (t + 1 < nsteps) ? t + 1 : nsteps - 1;
   const int64_t t2 = (t + 2 < nsteps) ? t + 2 : nsteps - 1;
@@ -246,60 +282,74 @@ __device__ __forceinline__ void gemm_step(const GemmArgs &g, const Producer &pro
   Lut16 lut;
   WordLookup wl;
   uint32_t wout[2][4];
-  u32x4 a[2][4], b[2][4];
+  // Fragment-read pair p of sub-step s into buffer n.
+  auto read_pair = [&](int s, int p, int n) {
+    const int u = 2 * s + grp;
+    if (p < 2) {
+      a[n][2 * p] = Acur[lds_unit(64 * p + jl, u)];
+      a[n][2 * p + 1] = Acur[lds_unit(64 * p + 32 + jl, u)];
+    } else {
+      b[n][2 * (p - 2)] = Bcur[lds_unit_b(64 * (p - 2) + jl, u)];
+      b[n][2 * (p - 2) + 1] = Bcur[lds_unit_b(64 * (p - 2) + 32 + jl, u)];
+    }
+  };
+  auto dma = [&](int d) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(arsrc, (lds_void_t *)(Anext_wave + d * 64), 16,
+                                             (int)aoff[d], (int)(t1 * (kStep * 2)), 0, 0);
+  };
+  auto word_stage = [&](int k, int stage) {
+    if (stage == 0) word_select(words[k], wl);
+    if (stage == 1) word_even(lut, wl);
+    if (stage == 2) word_odd(lut, wl);
+    if (stage == 3) {
+      Producer::merge(wl, wout[k & 1]);
+      if (Producer::kStoreParts == 1) prod.store(Bnext, wout[k & 1], k, 0);
+    }
+  };
+  auto store_part = [&](int k, int p) {
+    if (Producer::kStoreParts > 1) prod.store(Bnext, wout[k & 1], k, p);
+  };
+  // Previous step's tail, then this step's sub-step 0 fragments.
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int row = 32 * i + jl;
-    a[0][i] = Acur[lds_unit(row, grp)];
-    b[0][i] = Bcur[lds_unit_b(row, grp)];
+    acc[3][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+        __builtin_bit_cast(bf16x8, a[1][3]), __builtin_bit_cast(bf16x8, b[1][i]), acc[3][i], 0,
+        0, 0);
+    read_pair(0, i, 0);
+    if (i == 3) prod.load(g, t2, wn_, an_);
+    __builtin_amdgcn_sched_barrier(0);
   }
-  prod.load(g, t2, wn_, an_);
-  __builtin_amdgcn_sched_barrier(0);
-  // Slot plan after MFMA i of sub-step s:
-  //   i 0-3   (s < 3) two fragment reads of sub-step s+1
-  //   i 4-7   one activation DMA (4s + i - 4); for s = 1 also stores of word 0
-  //           when the producer writes a word in parts
-  //   i 8-11  s = 0: product-table quarters; s > 0: lookup stages of word s
-  //   i 12-15 s = 0: lookup stages of word 0; s > 0: parts of word s's store
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
     const int n = (s + 1) & 1;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
+    for (int i = 0; i < ((s == 3) ? 12 : 16); ++i) {
       const int mt = i >> 2, nt = i & 3;
       acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
           __builtin_bit_cast(bf16x8, a[s & 1][mt]), __builtin_bit_cast(bf16x8, b[s & 1][nt]),
           acc[mt][nt], 0, 0, 0);
-      if (s < 3 && i < 4) {
-        const int u = 2 * (s + 1) + grp;
-        if (i < 2) {
-          a[n][2 * i] = Acur[lds_unit(64 * i + jl, u)];
-          a[n][2 * i + 1] = Acur[lds_unit(64 * i + 32 + jl, u)];
-        } else {
-          b[n][2 * (i - 2)] = Bcur[lds_unit_b(64 * (i - 2) + jl, u)];
-          b[n][2 * (i - 2) + 1] = Bcur[lds_unit_b(64 * (i - 2) + 32 + jl, u)];
-        }
-      }
-      if (i >= 4 && i < 8) {
-        const int d = 4 * s + (i - 4);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(arsrc, (lds_void_t *)(Anext_wave + d * 64), 16,
-                                                 (int)aoff[d], (int)(t1 * (kStep * 2)), 0, 0);
-        if (Producer::kStoreParts > 1 && s == 1) prod.store(Bnext, wout[0], 0, i - 4);
-      }
-      const int stage = (s == 0) ? i - 12 : i - 8;  // lookup stage of word s
-      if (s == 0 && i >= 8 && i < 12) make_lut_quarter<false>(ta, i - 8, lut);
-      if (stage == 0) word_select(words[s], wl);
-      if (stage == 1) word_even(lut, wl);
-      if (stage == 2) word_odd(lut, wl);
-      if (stage == 3) {
-        Producer::merge(wl, wout[s & 1]);
-        if (Producer::kStoreParts == 1) prod.store(Bnext, wout[s & 1], s, 0);
-      }
-      if (Producer::kStoreParts > 1 && s > 0 && i >= 12)
-        prod.store(Bnext, wout[s & 1], s, i - 12);
+      const int q = i & 3;  // position inside the slot group
+      if (s < 3 && i < 4) read_pair(s + 1, q, n);
+      if (s < 2 && i < 4) dma(8 * s + q);
+      if (s < 2 && i >= 12) dma(8 * s + 4 + q);
+      if (s == 0 && i >= 4 && i < 8) make_lut_quarter<false>(ta, q, lut);
+      if (s == 0 && i >= 8 && i < 12) word_stage(0, q);
+      if (s > 0 && i >= 4 && i < 8) word_stage(s, q);
+      if (s > 0 && i >= 8 && i < 12) store_part(s - 1 + (s == 3 ? 1 : 0), q);
+      if (s == 3 && i < 4) store_part(2, q);
       __builtin_amdgcn_sched_barrier(0);
     }
   }
+}
+
+// The last step's tail (see gemm_step).
+__device__ __forceinline__ void gemm_tail(floatx16 (&acc)[4][4], const u32x4 (&a)[2][4],
+                                          const u32x4 (&b)[2][4]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    acc[3][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+        __builtin_bit_cast(bf16x8, a[1][3]), __builtin_bit_cast(bf16x8, b[1][i]), acc[3][i], 0,
+        0, 0);
 }
 
 template <class Producer>
@@ -363,15 +413,23 @@ __global__ void __launch_bounds__(kGemmThreads, 1) nf4_gemm_kernel(const GemmArg
                                              0, 0, 0);
   {
     u32x4 w0;
-    float s0;
+    AbsRaw s0;
     prod.load(g, 0, w0, s0);
     prod.store(g_lds_b0, w0, s0);
   }
   u32x4 wc, wn;
-  float ac, an;
+  AbsRaw ac, an;
   prod.load(g, nsteps > 1 ? 1 : 0, wc, ac);
   __builtin_amdgcn_s_waitcnt(0);  // the DMA of step 0 has landed in LDS
   __syncthreads();
+
+  // Fragment registers; the first step's tail multiplies zeros.
+  u32x4 fa[2][4], fb[2][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    fa[1][i] = (u32x4){0u, 0u, 0u, 0u};
+    fb[1][i] = (u32x4){0u, 0u, 0u, 0u};
+  }
 
   // One loop body for every step; the buffers alternate by step parity.
   // The last step's "next" work reads clamped (valid) addresses and fills
@@ -379,15 +437,16 @@ __global__ void __launch_bounds__(kGemmThreads, 1) nf4_gemm_kernel(const GemmArg
 #pragma unroll 1
   for (int64_t t = 0; t < nsteps; ++t) {
     const bool odd = (t & 1) != 0;
-    gemm_step<Producer>(g, prod, acc, odd ? a1w : a0w, odd ? a0w : a1w, odd ? g_lds_b1 : g_lds_b0,
-                        odd ? g_lds_b0 : g_lds_b1, arsrc, aoff, wc, ac, wn, an, t, nsteps, jl,
-                        grp);
+    gemm_step<Producer>(g, prod, acc, fa, fb, odd ? a1w : a0w, odd ? a0w : a1w,
+                        odd ? g_lds_b1 : g_lds_b0, odd ? g_lds_b0 : g_lds_b1, arsrc, aoff, wc, ac,
+                        wn, an, t, nsteps, jl, grp);
     // Next step's activation tile (direct-to-LDS) and weight tile complete.
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     wc = wn;
     ac = an;
   }
+  gemm_tail(acc, fa, fb);
 
   // Epilogue: fp32 -> bf16 (RNE).  Lane l holds column o0 + 32nt + l%32 of
   // rows m0 + 32mt + 8(v/4) + 4g + v%4; one 64-bit base pointer per lane,
