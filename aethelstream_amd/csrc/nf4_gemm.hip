@@ -23,7 +23,9 @@
 // and 8 reduction slots from lane group g = l / 32.  The kernel assigns
 // reduction index 32g + 8s + e to slot e of sub-step s for BOTH operands, so
 // a lane's 4 sub-steps read 64 contiguous bytes of its activation row.  The
-// accumulator layout is lane l: column l % 32, row 8(v/4) + 4g + v%4.
+// accumulator layout is lane l: column l % 32, row 8(v/4) + 4g + v%4; the
+// weight fragment is the first operand, so the accumulator's columns are
+// activation rows and its rows are output columns.
 #include "abi_common.hpp"
 #include "nf4_device.hpp"
 
@@ -313,7 +315,7 @@ __device__ __forceinline__ void gemm_step(const GemmArgs &g, const Producer &pro
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     acc[3][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-        __builtin_bit_cast(bf16x8, a[1][3]), __builtin_bit_cast(bf16x8, b[1][i]), acc[3][i], 0,
+        __builtin_bit_cast(bf16x8, b[1][i]), __builtin_bit_cast(bf16x8, a[1][3]), acc[3][i], 0,
         0, 0);
     read_pair(0, i, 0);
     if (i == 3) prod.load(g, t2, wn_, an_);
@@ -326,7 +328,7 @@ __device__ __forceinline__ void gemm_step(const GemmArgs &g, const Producer &pro
     for (int i = 0; i < ((s == 3) ? 12 : 16); ++i) {
       const int mt = i >> 2, nt = i & 3;
       acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-          __builtin_bit_cast(bf16x8, a[s & 1][mt]), __builtin_bit_cast(bf16x8, b[s & 1][nt]),
+          __builtin_bit_cast(bf16x8, b[s & 1][nt]), __builtin_bit_cast(bf16x8, a[s & 1][mt]),
           acc[mt][nt], 0, 0, 0);
       const int q = i & 3;  // position inside the slot group
       if (s < 3 && i < 4) read_pair(s + 1, q, n);
@@ -348,7 +350,7 @@ __device__ __forceinline__ void gemm_tail(floatx16 (&acc)[4][4], const u32x4 (&a
 #pragma unroll
   for (int i = 0; i < 4; ++i)
     acc[3][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-        __builtin_bit_cast(bf16x8, a[1][3]), __builtin_bit_cast(bf16x8, b[1][i]), acc[3][i], 0,
+        __builtin_bit_cast(bf16x8, b[1][i]), __builtin_bit_cast(bf16x8, a[1][3]), acc[3][i], 0,
         0, 0);
 }
 
@@ -448,28 +450,37 @@ __global__ void __launch_bounds__(kGemmThreads, 1) nf4_gemm_kernel(const GemmArg
   }
   gemm_tail(acc, fa, fb);
 
-  // Epilogue: fp32 -> bf16 (RNE).  Lane l holds column o0 + 32nt + l%32 of
-  // rows m0 + 32mt + 8(v/4) + 4g + v%4; one 64-bit base pointer per lane,
-  // uniform row offsets, 32-bit bounds.
-  const int64_t row0 = m0 + 4 * grp;
-  const int64_t rl = g.M - row0;
-  const int64_t cl = g.O - (o0 + jl);
-  const int32_t rlim = (int32_t)(rl < 0 ? 0 : (rl > (1 << 30) ? (1 << 30) : rl));
+  // Epilogue: fp32 -> bf16 (RNE).  The MFMAs take the weight fragment as
+  // their first operand, so each accumulator tile is the transposed output
+  // block: lane l holds activation row m0 + 32mt + l%32 and output columns
+  // o0 + 32nt + 8j + 4g + i (i = 0..3) in registers 4j + i.  Four adjacent
+  // columns leave as one 8-byte store.
+  const bool vec_ok = ((reinterpret_cast<uintptr_t>(g.out) & 7) == 0) && ((g.ldo & 3) == 0);
+  const int64_t cl = g.O - (o0 + 4 * grp);
   const int32_t clim = (int32_t)(cl < 0 ? 0 : (cl > (1 << 30) ? (1 << 30) : cl));
-  uint16_t *obase = g.out + (row0 < g.M ? row0 : 0) * g.ldo + o0 + jl;
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt)
+  for (int mt = 0; mt < 4; ++mt) {
+    const int64_t m = m0 + 32 * mt + jl;
+    if (m < g.M) {
+      uint16_t *orow = g.out + m * g.ldo + o0 + 4 * grp;
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const int r = 32 * mt + 8 * (v >> 2) + (v & 3);
-      if (r < rlim) {
-        uint16_t *orow = obase + (int64_t)r * g.ldo;
+      for (int nt = 0; nt < 4; ++nt)
 #pragma unroll
-        for (int nt = 0; nt < 4; ++nt)
-          if (32 * nt < clim)
-            orow[32 * nt] = __builtin_bit_cast(uint16_t, (__bf16)acc[mt][nt][v]);
-      }
+        for (int j = 0; j < 4; ++j) {
+          const int c = 32 * nt + 8 * j;
+          const uint32_t lo = pack_bf16x2(acc[mt][nt][4 * j], acc[mt][nt][4 * j + 1]);
+          const uint32_t hi = pack_bf16x2(acc[mt][nt][4 * j + 2], acc[mt][nt][4 * j + 3]);
+          if (vec_ok && c + 4 <= clim) {
+            *reinterpret_cast<u32x2 *>(orow + c) = (u32x2){lo, hi};
+          } else {
+            if (c < clim) orow[c] = (uint16_t)(lo & 0xffffu);
+            if (c + 1 < clim) orow[c + 1] = (uint16_t)(lo >> 16);
+            if (c + 2 < clim) orow[c + 2] = (uint16_t)(hi & 0xffffu);
+            if (c + 3 < clim) orow[c + 3] = (uint16_t)(hi >> 16);
+          }
+        }
     }
+  }
 }
 
 static AbsmaxRef absmax_of(const nf4s_tensor &t) {
