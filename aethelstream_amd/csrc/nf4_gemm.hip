@@ -228,12 +228,13 @@ __device__ __forceinline__ void map_tile(int tiles_m, int tiles_o, int &tm, int 
   to = L - tm * tiles_o;
 }
 
-// LDS: two activation buffers (per wave 128 rows x 128 B = 16 KB; 4 waves =
-// 64 KB each) and two weight tiles (16 KB each): 160 KB, the gfx950 maximum.
-__shared__ u32x4 g_lds_a0[4 * 1024];
-__shared__ u32x4 g_lds_a1[4 * 1024];
-__shared__ u32x4 g_lds_b0[1024];
-__shared__ u32x4 g_lds_b1[1024];
+// LDS: two activation buffers per wave (128 rows x 128 B = 16 KB each, a
+// wave's pair adjacent) and two weight tiles (16 KB each): 160 KB, the gfx950
+// maximum.  With the buffers of a pair 16 KB apart, the main loop (unrolled
+// by two steps) addresses both through the LDS instructions' immediate
+// offsets from loop-invariant lane addresses.
+__shared__ u32x4 g_lds_a[4][2][1024];
+__shared__ u32x4 g_lds_b[2][1024];
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
@@ -404,8 +405,8 @@ __global__ void __launch_bounds__(kGemmThreads, 1) nf4_gemm_kernel(const GemmArg
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[mt][nt][v] = 0.0f;
 
-  u32x4 *a0w = g_lds_a0 + wave * 1024;
-  u32x4 *a1w = g_lds_a1 + wave * 1024;
+  u32x4 *a0w = &g_lds_a[wave][0][0];
+  u32x4 *a1w = &g_lds_a[wave][1][0];
 
   // Prologue: activation tile of step 0 (DMA), weight tile of step 0
   // (dequantized into b0), packed weights of step 1 in registers.
@@ -417,7 +418,7 @@ __global__ void __launch_bounds__(kGemmThreads, 1) nf4_gemm_kernel(const GemmArg
     u32x4 w0;
     AbsRaw s0;
     prod.load(g, 0, w0, s0);
-    prod.store(g_lds_b0, w0, s0);
+    prod.store(g_lds_b[0], w0, s0);
   }
   u32x4 wc, wn;
   AbsRaw ac, an;
@@ -433,20 +434,27 @@ __global__ void __launch_bounds__(kGemmThreads, 1) nf4_gemm_kernel(const GemmArg
     fb[1][i] = (u32x4){0u, 0u, 0u, 0u};
   }
 
-  // One loop body for every step; the buffers alternate by step parity.
+  // Two steps per iteration, even then odd buffers; the packed-weight
+  // registers swap roles instead of being copied.  After each step the next
+  // step's activation tile (direct-to-LDS) and weight tile are complete.
   // The last step's "next" work reads clamped (valid) addresses and fills
   // buffers nobody reads again.
 #pragma unroll 1
-  for (int64_t t = 0; t < nsteps; ++t) {
-    const bool odd = (t & 1) != 0;
-    gemm_step<Producer>(g, prod, acc, fa, fb, odd ? a1w : a0w, odd ? a0w : a1w,
-                        odd ? g_lds_b1 : g_lds_b0, odd ? g_lds_b0 : g_lds_b1, arsrc, aoff, wc, ac,
-                        wn, an, t, nsteps, jl, grp);
-    // Next step's activation tile (direct-to-LDS) and weight tile complete.
+  for (int64_t t = 0; t + 1 < nsteps; t += 2) {
+    gemm_step<Producer>(g, prod, acc, fa, fb, a0w, a1w, g_lds_b[0], g_lds_b[1], arsrc, aoff, wc,
+                        ac, wn, an, t, nsteps, jl, grp);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    wc = wn;
-    ac = an;
+    gemm_step<Producer>(g, prod, acc, fa, fb, a1w, a0w, g_lds_b[1], g_lds_b[0], arsrc, aoff, wn,
+                        an, wc, ac, t + 1, nsteps, jl, grp);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+  if (nsteps & 1) {
+    gemm_step<Producer>(g, prod, acc, fa, fb, a0w, a1w, g_lds_b[0], g_lds_b[1], arsrc, aoff, wc,
+                        ac, wn, an, nsteps - 1, nsteps, jl, grp);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
   }
   gemm_tail(acc, fa, fb);
 
