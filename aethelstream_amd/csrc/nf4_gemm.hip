@@ -266,8 +266,10 @@ constexpr int kBufferFlags = 0x00020000;
 //   s=1: i0-3 R + D8-11  i4-7 W(1)     i8-11 P(0)    i12-15 D12-15
 //   s=2: i0-3 R          i4-7 W(2)     i8-11 P(1)
 //   s=3: i0-3 P(2)       i4-7 W(3)     i8-11 P(3)    -> barrier
-// The DMAs are all issued by the middle of the step, so they have landed
-// by the barrier.
+// The forward producer (no P jobs) issues its DMAs in slots 8-15 of
+// sub-steps 0 and 1 instead, away from the fragment reads (measured faster
+// for the forward, slower for dgrad).  The DMAs are all issued by the middle of the
+// step, so they have landed by the barrier.
 template <class Producer>
 __device__ __forceinline__ void gemm_step(const GemmArgs &g, const Producer &prod,
                                           floatx16 (&acc)[4][4], u32x4 (&a)[2][4],
@@ -333,8 +335,12 @@ __device__ __forceinline__ void gemm_step(const GemmArgs &g, const Producer &pro
           acc[mt][nt], 0, 0, 0);
       const int q = i & 3;  // position inside the slot group
       if (s < 3 && i < 4) read_pair(s + 1, q, n);
-      if (s < 2 && i < 4) dma(8 * s + q);
-      if (s < 2 && i >= 12) dma(8 * s + 4 + q);
+      if (Producer::kStoreParts == 1) {
+        if (s < 2 && i >= 8) dma(8 * s + (i - 8));
+      } else {
+        if (s < 2 && i < 4) dma(8 * s + q);
+        if (s < 2 && i >= 12) dma(8 * s + 4 + q);
+      }
       if (s == 0 && i >= 4 && i < 8) make_lut_quarter<false>(ta, q, lut);
       if (s == 0 && i >= 8 && i < 12) word_stage(0, q);
       if (s > 0 && i >= 4 && i < 8) word_stage(s, q);
