@@ -112,11 +112,20 @@ struct WordLookup {
 // turns bit 7 of every byte of v into a 0x00 / 0xff byte mask.
 constexpr uint32_t kSignBytes = 0x0B090A08u;
 
-__device__ __forceinline__ void word_select(uint32_t w, WordLookup &x) {
+// word_select in two halves: the 3-bit selectors, then the bit-3 masks.
+__device__ __forceinline__ void word_select_idx(uint32_t w, WordLookup &x) {
   x.selE = (w >> 4) & 0x07070707u;
   x.selO = w & 0x07070707u;
+}
+
+__device__ __forceinline__ void word_select_mask(uint32_t w, WordLookup &x) {
   x.maskE = perm(w, w << 8, kSignBytes);          // bit 3 of each high nibble
   x.maskO = perm(w << 4, w << 12, kSignBytes);    // bit 3 of each low nibble
+}
+
+__device__ __forceinline__ void word_select(uint32_t w, WordLookup &x) {
+  word_select_idx(w, x);
+  word_select_mask(w, x);
 }
 
 __device__ __forceinline__ void word_even(const Lut16 &t, WordLookup &x) {
@@ -140,13 +149,18 @@ __device__ __forceinline__ void word_pairs(const WordLookup &x, uint32_t pairs[4
   pairs[3] = perm(x.hiO, x.loO, 0x07030602u);
 }
 
-__device__ __forceinline__ void word_merge(const WordLookup &x, uint32_t out[4]) {
-  uint32_t p[4];
-  word_pairs(x, p);
+// Second half of the merge: natural element order from word_pairs' output.
+__device__ __forceinline__ void pairs_merge(const uint32_t p[4], uint32_t out[4]) {
   out[0] = perm(p[1], p[0], 0x05040100u);
   out[1] = perm(p[1], p[0], 0x07060302u);
   out[2] = perm(p[3], p[2], 0x05040100u);
   out[3] = perm(p[3], p[2], 0x07060302u);
+}
+
+__device__ __forceinline__ void word_merge(const WordLookup &x, uint32_t out[4]) {
+  uint32_t p[4];
+  word_pairs(x, p);
+  pairs_merge(p, out);
 }
 
 // Dequantize the 8 elements of one packed word w; out[j] = elem 2j |
@@ -157,6 +171,20 @@ __device__ __forceinline__ void lut_apply8(const Lut16 &t, uint32_t w, uint32_t 
   word_even(t, x);
   word_odd(t, x);
   word_merge(x, out);
+}
+
+// The product table built in 8 halves of quarters, for callers that
+// interleave it with other work: half h computes entries 2h and 2h+1 into
+// d[h & 1]; the odd half of quarter q then also forms lo[q] and hi[q].
+template <bool kF16>
+__device__ __forceinline__ void make_lut_half(float absmax, int h, uint32_t (&d)[2], Lut16 &t) {
+  const float p0 = fp32_rounded(code_value(2 * h) * absmax);
+  const float p1 = fp32_rounded(code_value(2 * h + 1) * absmax);
+  d[h & 1] = kF16 ? pack_f16x2(p0, p1) : pack_bf16x2(p0, p1);
+  if (h & 1) {
+    t.lo[h >> 1] = perm(d[1], d[0], 0x06040200u);
+    t.hi[h >> 1] = perm(d[1], d[0], 0x07050301u);
+  }
 }
 
 // The product table built in 4 quarters (entries 4q..4q+3 each), for callers

@@ -39,6 +39,20 @@ constexpr int kTileM = 512;   // activation rows per workgroup (128 per wave)
 constexpr int kTileO = 128;   // output columns per workgroup
 constexpr int kStep = 64;     // reduction depth per step (= NF4 block size)
 
+// Compile-time loop: f(IC<B>{}), ..., f(IC<E-1>{}).  Slot plans, fragment
+// indices and LDS immediate offsets are then constant expressions.
+template <int N>
+struct IC {
+  static constexpr int value = N;
+};
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F &&f) {
+  if constexpr (B < E) {
+    f(IC<B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
 struct GemmArgs {
   const uint16_t *a;  // activation [M, R] row-major (x or dy)
   int64_t lda;
@@ -52,17 +66,22 @@ struct GemmArgs {
   int32_t tiles_m, tiles_o;
 };
 
-// LDS tile: 128 rows x 64 bf16 (128 B = 8 units of 16 B).  Unit u of row r
-// lives at r*8 + (u ^ (r & 7)) so that the 32 rows a wave reads for one
-// fragment spread over all banks.
-__device__ __forceinline__ int lds_unit(int row, int u) { return row * 8 + (u ^ (row & 7)); }
+// LDS tile: 128 rows x 64 bf16 (128 B = 8 units of 16 B).  A 16-B access
+// (ds_read_b128, ds_write_b128) is served 16 lanes at a time, 256 B over the
+// 64 banks, and the lanes of one group cover 16 consecutive rows at one
+// logical unit.  Unit u of row r lives at r*8 + (u ^ swz(r)), where swz(r)
+// takes 8 distinct values over the even rows and over the odd rows of every
+// aligned group of 16 (and over every aligned group of 8 rows), so each
+// group of 16 lanes touches 16 distinct 16-B bank windows.
+__device__ __forceinline__ int swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
+__device__ __forceinline__ int lds_unit(int row, int u) { return row * 8 + (u ^ swz(row)); }
 
 // Weight tile: the same swizzle XOR 2 * ((row / 32) % 4).  The extra term is
-// constant over the 32 rows of one fragment read, so reads stay spread over
-// the banks, and it spreads the dgrad producer's 16-bit stores (whose lanes
-// cover output columns 32 apart) over all banks too.
+// constant over each aligned group of 16 rows, so fragment reads stay spread
+// over the banks, and it spreads the dgrad producer's 16-bit stores (whose
+// lanes cover output columns 32 apart) over all banks too.
 __device__ __forceinline__ int lds_unit_b(int row, int u) {
-  return row * 8 + (u ^ (row & 7) ^ ((row >> 4) & 6));
+  return row * 8 + (u ^ swz(row) ^ ((row >> 4) & 6));
 }
 
 // Lookup of packed word w with product table t, finished by the producer's
@@ -103,16 +122,20 @@ __device__ __forceinline__ float absmax_value(const AbsRaw &r) {
   return kDQ ? (float)r.q * r.s : r.s;
 }
 
-// Forward producer: thread -> (row n_local = tid/2, half h = tid%2), 32
-// consecutive k of one block; writes 4 swizzled 16-B units of its row.
+// Forward producer: thread -> (row n_local, half h), 32 consecutive k of one
+// block; writes 4 swizzled 16-B units of its row.  Lanes 16j..16j+15 of a
+// wave take 16 consecutive rows at one half, so each 16-lane group of a
+// ds_write_b128 covers 16 rows at one logical unit (no bank conflicts).
 template <bool kDQ>
 struct FwdProducer {
   const uint8_t *ptr;   // packed bytes of (row, half) at step 0
   int64_t am_idx;       // absmax block index at step 0
   int row, h;
-  __device__ void init(const GemmArgs &g, int64_t o0) {
-    row = threadIdx.x >> 1;
-    h = threadIdx.x & 1;
+  __device__ void init(const GemmArgs &g, int64_t o0, uint32_t b0_lds) {
+    (void)b0_lds;
+    const int lane = threadIdx.x & 63;
+    row = 32 * (threadIdx.x >> 6) + 16 * (lane >> 5) + (lane & 15);
+    h = (lane >> 4) & 1;
     int64_t n = o0 + row;
     if (n >= g.wn) n = g.wn - 1;  // ragged N: clamp (outputs are not stored)
     ptr = g.packed + n * (g.wk >> 1) + 16 * h;
@@ -133,8 +156,8 @@ struct FwdProducer {
   // Writes the 8 dequantized elements of packed word k in `part` of
   // kStoreParts.
   static constexpr int kStoreParts = 1;
-  __device__ __forceinline__ void store(u32x4 *lds, const uint32_t out[4], int k, int part) const {
-    (void)part;
+  template <int kPar, int k, int kPart>
+  __device__ __forceinline__ void store(u32x4 *lds, const uint32_t out[4]) const {
     u32x4 v;
     v.x = out[0]; v.y = out[1]; v.z = out[2]; v.w = out[3];
     lds[lds_unit_b(row, 4 * h + k)] = v;
@@ -143,12 +166,12 @@ struct FwdProducer {
   __device__ __forceinline__ void store(u32x4 *lds, const u32x4 &w, const AbsRaw &a) const {
     const Lut16 lut = make_lut<false>(table_absmax(a));
     const uint32_t words[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
+    static_for<0, 4>([&](auto K) {
+      constexpr int k = decltype(K)::value;
       uint32_t o[4];
       dequant_word<FwdProducer>(lut, words[k], o);
-      store(lds, o, k, 0);
-    }
+      this->template store<0, k, 0>(lds, o);
+    });
   }
 };
 
@@ -157,15 +180,30 @@ struct FwdProducer {
 // q = tid%4): 32 consecutive columns of one block.  The LDS tile is stored
 // transposed (LDS row = output column, 64 reduction values per row), so
 // each element is written as one 16-bit value.
+//
+// With col = 32q + 8k + j (packed word k, element j), the byte address of
+// element (col, r) in the weight tile (lds_unit_b) is
+//   (8k + j) * 128 + sbase[j ^ (k & 1)],
+//   sbase[c] = 4096q + 16 * ((r / 8) ^ 2q ^ c) + 2 * (r % 8),
+// so each store is one of 8 per-thread addresses plus an immediate offset.
+// The stores are written as inline asm: the compiler then does not treat
+// them as LDS accesses that may alias the activation DMAs in flight (it
+// would wait for those, vmcnt(0), before every store).  Their completion is
+// covered by the explicit lgkmcnt(0) before each step's barrier.
 template <bool kDQ>
 struct DgradProducer {
   const uint8_t *ptr;
   int64_t am_idx;
   int r, q;
   uint32_t valid_mask;  // all ones when the thread's columns exist
-  __device__ void init(const GemmArgs &g, int64_t o0) {
+  uint32_t sbase[8];    // LDS byte addresses in weight buffer 0 (see above)
+  __device__ void init(const GemmArgs &g, int64_t o0, uint32_t b0_lds) {
     r = threadIdx.x >> 2;
     q = threadIdx.x & 3;
+#pragma unroll
+    for (int c = 0; c < 8; ++c)
+      sbase[c] = b0_lds + 4096u * (uint32_t)q + 16u * (uint32_t)((r >> 3) ^ (2 * q) ^ c) +
+                 2u * (uint32_t)(r & 7);
     const int64_t col = o0 + 32 * q;
     const bool valid = col < g.wk;
     valid_mask = valid ? 0xffffffffu : 0u;
@@ -189,28 +227,34 @@ struct DgradProducer {
   }
   // Writes the 8 elements of packed word k as 16-bit values down 8 LDS rows
   // (output columns); part p of 4 writes elements 2p and 2p+1.
+  // Weight buffer kPar (0 or 1, 16 KB apart) is the destination.
   static constexpr int kStoreParts = 4;
-  __device__ __forceinline__ void store(u32x4 *lds, const uint32_t out[4], int k, int part) const {
-    uint16_t *l16 = reinterpret_cast<uint16_t *>(lds);
-#pragma unroll
-    for (int jj = 0; jj < 2; ++jj) {
-      const int j = 2 * part + jj;
-      const int col = 32 * q + 8 * k + j;  // LDS row (output column)
+  template <int kPar, int k, int kPart>
+  __device__ __forceinline__ void store(u32x4 *lds, const uint32_t out[4]) const {
+    (void)lds;
+    static_for<0, 2>([&](auto JJ) {
+      constexpr int j = 2 * kPart + decltype(JJ)::value;
+      constexpr int off = kPar * 16384 + (8 * k + j) * 128;
       const uint32_t pr = out[(j & 1) + 2 * (j >> 2)];
-      const uint16_t v = (uint16_t)(((j >> 1) & 1) ? (pr >> 16) : (pr & 0xffffu));
-      l16[lds_unit_b(col, r >> 3) * 8 + (r & 7)] = v;
-    }
+      const uint32_t a = sbase[j ^ (k & 1)];
+      if constexpr (((j >> 1) & 1) == 0)
+        asm volatile("ds_write_b16 %0, %1 offset:%2" ::"v"(a), "v"(pr), "i"(off) : "memory");
+      else
+        asm volatile("ds_write_b16_d16_hi %0, %1 offset:%2" ::"v"(a), "v"(pr), "i"(off) : "memory");
+    });
   }
   __device__ __forceinline__ void store(u32x4 *lds, const u32x4 &w, const AbsRaw &a) const {
     const Lut16 lut = make_lut<false>(table_absmax(a));
     const uint32_t words[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
+    static_for<0, 4>([&](auto K) {
+      constexpr int k = decltype(K)::value;
       uint32_t o[4];
       dequant_word<DgradProducer>(lut, words[k], o);
-#pragma unroll
-      for (int p = 0; p < 4; ++p) store(lds, o, k, p);
-    }
+      this->template store<0, k, 0>(lds, o);
+      this->template store<0, k, 1>(lds, o);
+      this->template store<0, k, 2>(lds, o);
+      this->template store<0, k, 3>(lds, o);
+    });
   }
 };
 
@@ -241,124 +285,289 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 // Word 3 of a raw (stride 0) gfx9 buffer resource: 32-bit data format.
 constexpr int kBufferFlags = 0x00020000;
 
-// One 64-deep reduction step: 4 sub-steps of 16 MFMAs over the activation
-// tile in Acur (this wave's rows) and the weight tile in Bcur.  Alongside it
-//   * starts the direct-to-LDS loads of the next step's activation tile into
-//     Anext (16 instructions of 1 KB, 8 full 128-B rows each),
-//   * loads the packed weight bytes of step t+2 (wn_, an_),
-//   * dequantizes step t+1's weights (wc, ac) into Bnext,
-//   * prefetches the next sub-step's A and B fragments.
-// A wave issues in order, so other work only overlaps the matrix pipe when
-// it sits between MFMAs in the instruction stream: every MFMA is followed by
-// one small piece of that work (a few VALU ops, two LDS reads, a DMA), and
-// sched_barrier fences keep that order.
-//
-// The step ends at the workgroup barrier after MFMA 11 of sub-step 3; its
-// last 4 MFMAs (a[1][3] x b[1][0..3], operands already in registers) open
-// the NEXT call, after the barrier, each followed by one pair of fragment
-// reads of the new step's sub-step 0, so those reads' latency hides behind
-// matrix work.  The first call runs them on zero operands.
-//
-// Slot plan, after MFMA i of sub-step s (R = fragment-read pair for s+1,
-// D = activation DMA, L = product-table quarter, W = lookup stage of a
-// packed word, P = part of a word's 16-bit transposed store):
-//   s=0: i0-3 R + D0-3   i4-7 L0-3     i8-11 W(0)    i12-15 D4-7
-//   s=1: i0-3 R + D8-11  i4-7 W(1)     i8-11 P(0)    i12-15 D12-15
-//   s=2: i0-3 R          i4-7 W(2)     i8-11 P(1)
-//   s=3: i0-3 P(2)       i4-7 W(3)     i8-11 P(3)    -> barrier
-// The forward producer (no P jobs) issues its DMAs in slots 8-15 of
-// sub-steps 0 and 1 instead, away from the fragment reads (measured faster
-// for the forward, slower for dgrad).  The DMAs are all issued by the middle of the
-// step, so they have landed by the barrier.
-template <class Producer>
-__device__ __forceinline__ void gemm_step(const GemmArgs &g, const Producer &prod,
-                                          floatx16 (&acc)[4][4], u32x4 (&a)[2][4],
-                                          u32x4 (&b)[2][4], const u32x4 *__restrict__ Acur,
-                                          u32x4 *__restrict__ Anext_wave,
-                                          const u32x4 *__restrict__ Bcur,
-                                          u32x4 *__restrict__ Bnext,
-                                          __amdgpu_buffer_rsrc_t arsrc, const uint32_t (&aoff)[16],
-                                          const u32x4 &wc, const AbsRaw &ac, u32x4 &wn_, AbsRaw &an_,
-                                          int64_t t, int64_t nsteps, int jl, int grp) {
-  const int64_t t1 = (t + 1 < nsteps) ? t + 1 : nsteps - 1;
-  const int64_t t2 = (t + 2 < nsteps) ? t + 2 : nsteps - 1;
-  const uint32_t words[4] = {wc.x, wc.y, wc.z, wc.w};
-  const float ta = prod.table_absmax(ac);
-  Lut16 lut;
-  WordLookup wl;
-  uint32_t wout[2][4];
-  // Fragment-read pair p of sub-step s into buffer n.
-  auto read_pair = [&](int s, int p, int n) {
-    const int u = 2 * s + grp;
-    if (p < 2) {
-      a[n][2 * p] = Acur[lds_unit(64 * p + jl, u)];
-      a[n][2 * p + 1] = Acur[lds_unit(64 * p + 32 + jl, u)];
-    } else {
-      b[n][2 * (p - 2)] = Bcur[lds_unit_b(64 * (p - 2) + jl, u)];
-      b[n][2 * (p - 2) + 1] = Bcur[lds_unit_b(64 * (p - 2) + 32 + jl, u)];
-    }
-  };
-  auto dma = [&](int d) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(arsrc, (lds_void_t *)(Anext_wave + d * 64), 16,
-                                             (int)aoff[d], (int)(t1 * (kStep * 2)), 0, 0);
-  };
-  auto word_stage = [&](int k, int stage) {
-    if (stage == 0) word_select(words[k], wl);
-    if (stage == 1) word_even(lut, wl);
-    if (stage == 2) word_odd(lut, wl);
-    if (stage == 3) {
-      Producer::merge(wl, wout[k & 1]);
-      if (Producer::kStoreParts == 1) prod.store(Bnext, wout[k & 1], k, 0);
-    }
-  };
-  auto store_part = [&](int k, int p) {
-    if (Producer::kStoreParts > 1) prod.store(Bnext, wout[k & 1], k, p);
-  };
-  // Previous step's tail, then this step's sub-step 0 fragments.
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    acc[3][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-        __builtin_bit_cast(bf16x8, b[1][i]), __builtin_bit_cast(bf16x8, a[1][3]), acc[3][i], 0,
-        0, 0);
-    read_pair(0, i, 0);
-    if (i == 3) prod.load(g, t2, wn_, an_);
-    __builtin_amdgcn_sched_barrier(0);
-  }
-#pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    const int n = (s + 1) & 1;
-#pragma unroll
-    for (int i = 0; i < ((s == 3) ? 12 : 16); ++i) {
-      const int mt = i >> 2, nt = i & 3;
-      acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-          __builtin_bit_cast(bf16x8, b[s & 1][nt]), __builtin_bit_cast(bf16x8, a[s & 1][mt]),
-          acc[mt][nt], 0, 0, 0);
-      const int q = i & 3;  // position inside the slot group
-      if (s < 3 && i < 4) read_pair(s + 1, q, n);
-      if (Producer::kStoreParts == 1) {
-        if (s < 2 && i >= 8) dma(8 * s + (i - 8));
-      } else {
-        if (s < 2 && i < 4) dma(8 * s + q);
-        if (s < 2 && i >= 12) dma(8 * s + 4 + q);
-      }
-      if (s == 0 && i >= 4 && i < 8) make_lut_quarter<false>(ta, q, lut);
-      if (s == 0 && i >= 8 && i < 12) word_stage(0, q);
-      if (s > 0 && i >= 4 && i < 8) word_stage(s, q);
-      if (s > 0 && i >= 8 && i < 12) store_part(s - 1 + (s == 3 ? 1 : 0), q);
-      if (s == 3 && i < 4) store_part(2, q);
-      __builtin_amdgcn_sched_barrier(0);
-    }
+// s_waitcnt immediates (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] |
+// lgkmcnt[11:8] | vmcnt[5:4] << 14).
+constexpr int kWaitLgkm0 = 0xC07F;       // lgkmcnt(0), vmcnt and expcnt not waited
+constexpr int kWaitVm8Lgkm0 = 0x0078;    // vmcnt(8) lgkmcnt(0)
+
+// Workgroup barrier without the memory-model fences of __syncthreads(): the
+// release fence would wait for every outstanding load (vmcnt(0)), including
+// the activation DMAs that are meant to stay in flight across it.  The waits
+// the barrier needs are issued explicitly before it (all but the 8 most
+// recent vector-memory operations, and every LDS operation); the empty asm
+// keeps the compiler from moving memory operations across it.
+__device__ __forceinline__ void step_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_waitcnt(kWaitVm8Lgkm0);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// Makes x opaque at this point of the instruction stream: arithmetic that
+// uses it cannot be scheduled before the (volatile, ordered) empty asm.
+__device__ __forceinline__ void pin(uint32_t &x) { asm volatile("" : "+v"(x)); }
+__device__ __forceinline__ void pin(float &x) { asm volatile("" : "+v"(x)); }
+
+// Fragment read k (0..7) of sub-step s into register buffer n, in the order
+// the sub-step's first MFMAs consume them: A0, B0, B1, B2, B3, A1, A2, A3.
+// Fragment j of A (B) holds rows 32j + jl of the activation (weight) tile.
+__device__ __forceinline__ void read_frag(const u32x4 *__restrict__ Acur,
+                                          const u32x4 *__restrict__ Bcur, u32x4 (&a)[2][4],
+                                          u32x4 (&b)[2][4], int s, int k, int n, int jl, int grp) {
+  const int u = 2 * s + grp;
+  if (k == 0 || k >= 5) {
+    const int j = (k == 0) ? 0 : k - 4;
+    a[n][j] = Acur[lds_unit(32 * j + jl, u)];
+  } else {
+    const int j = k - 1;
+    b[n][j] = Bcur[lds_unit_b(32 * j + jl, u)];
   }
 }
 
-// The last step's tail (see gemm_step).
+// The per-step slot plan.  Slot n = 16 s + i follows MFMA i of sub-step s;
+// sub-step 3 has 8 slots before the barrier, so a step has 56.  Job kinds:
+//   R  two fragment reads of the next sub-step (slots 0-3 of sub-steps 0-2);
+//      'n' is R plus an N job
+//   L  one half-quarter of the product table (2 products, 1 conversion)
+//   W  one lookup stage of a packed word, in order: selectors, masks, even
+//      elements, odd elements, pairs and (forward only) natural order plus
+//      the 16-B store
+//   N  one activation DMA of the NEXT step's tile, rows 64-127, into the
+//      other buffer
+//   A  one activation DMA of the step after next (t+2), rows 0-63, into the
+//      current buffer once this wave's reads of it have returned
+// In the dgrad plan some N/A slots also carry a P job: half of one word's
+// 16-bit transposed stores (dgrad_p_slot).  Each slot holds about the issue
+// time of one MFMA (32 cycles), and the 16 DMAs are spread over the step so
+// that the four waves of a CU never flood its texture-address unit.
+constexpr char kPlanFwd[57] =
+    "RnRnLLNLLNLLNLLN"
+    "RnRnWWWWWWWWWWWW"
+    "RRRRWWAWWAWWAWWA"
+    "WWAWAWAA";
+constexpr char kPlanDgrad[57] =
+    "RRRRLNLLNLLNLLNL"
+    "RRRRWNWWNWWNWWNW"
+    "RRRRWWWWAWWAWWAW"
+    "AWAWAWAA";
+constexpr bool dgrad_p_slot(int n) {
+  return n == 27 || n == 30 || n == 40 || n == 43 || n == 46 || n == 48 || n == 54 || n == 55;
+}
+// Number of jobs of kind c (of ('N' or 'n') when c is 'N') before slot n.
+constexpr int plan_index(const char *plan, int n, char c) {
+  int k = 0;
+  for (int i = 0; i < n; ++i) k += (plan[i] == c) || (c == 'N' && plan[i] == 'n');
+  return k;
+}
+constexpr int p_index(int n) {
+  int k = 0;
+  for (int i = 0; i < n; ++i) k += dgrad_p_slot(i);
+  return k;
+}
+
+// One 64-deep reduction step t: 4 sub-steps of 16 MFMAs over the activation
+// tile in Acur (this wave's 128 rows) and the weight tile in Bcur.  Alongside
+// the MFMAs it reads the next sub-step's fragments, dequantizes step t+1's
+// packed weights (wc, ac, loaded a step ago) into Bnext, loads the packed
+// weights of step t+2 (wn_, an_) and moves activation rows into LDS with
+// direct-to-LDS loads (1 KB = 8 whole 128-B rows per instruction): rows
+// 64-127 of step t+1 into Aoth (read last in step t-1) and rows 0-63 of step
+// t+2 into Acur after this wave's last reads of it.  Every DMA has at least
+// a sub-step to land before the barrier that precedes its reads, and the
+// barrier waits for all but the 8 most recent vector-memory operations.
+// A wave issues in order, so other work only overlaps the matrix pipe when
+// it sits between MFMAs; sched_barrier fences keep the slot plan's order.
+//
+// The step's barrier comes after MFMA 7 of sub-step 3.  The last 8 MFMAs
+// (a[1][2..3] x b[1][0..3], operands already in registers) open the NEXT
+// call, after the barrier, each followed by one fragment read of the new
+// step's sub-step 0.  The first call runs them on zero operands.
+template <class Producer, int kPar>
+__device__ __forceinline__ void gemm_step(const GemmArgs &g, const Producer &prod,
+                                          floatx16 (&acc)[4][4], u32x4 (&a)[2][4],
+                                          u32x4 (&b)[2][4], u32x4 *Acur, u32x4 *Aoth,
+                                          const u32x4 *Bcur, u32x4 *Bnext,
+                                          __amdgpu_buffer_rsrc_t arsrc, const uint32_t (&aoff)[16],
+                                          const u32x4 &wc, const AbsRaw &ac, u32x4 &wn_, AbsRaw &an_,
+                                          int64_t t, int64_t nsteps, int jl, int grp) {
+  constexpr bool kFwd = Producer::kStoreParts == 1;
+  constexpr int kWordStages = kFwd ? 6 : 5;
+  const int64_t t1 = (t + 1 < nsteps) ? t + 1 : nsteps - 1;
+  const int64_t t2 = (t + 2 < nsteps) ? t + 2 : nsteps - 1;
+  const uint32_t words[4] = {wc.x, wc.y, wc.z, wc.w};
+  Lut16 lut;
+  uint32_t lutd[2];
+  WordLookup wl;
+  uint32_t wp[4][4];  // word_pairs output of each packed word
+  float ta = 0.0f;
+  auto dma = [&](u32x4 *dst, int d, int64_t step) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(arsrc, (lds_void_t *)(dst + d * 64), 16,
+                                             (int)aoff[d], (int)(step * (kStep * 2)), 0, 0);
+  };
+
+  // Previous step's last 8 MFMAs, then this step's sub-step 0 fragments.
+  static_for<0, 8>([&](auto I) {
+    constexpr int i = decltype(I)::value;
+    constexpr int mt = 2 + (i >> 2), nt = i & 3;
+    acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+        __builtin_bit_cast(bf16x8, b[1][nt]), __builtin_bit_cast(bf16x8, a[1][mt]),
+        acc[mt][nt], 0, 0, 0);
+    read_frag(Acur, Bcur, a, b, 0, i, 0, jl, grp);
+    if constexpr (i == 3) prod.load(g, t2, wn_, an_);
+    if constexpr (i == 6) ta = prod.table_absmax(ac);
+    __builtin_amdgcn_sched_barrier(0);
+  });
+  static_for<0, 56>([&](auto N) {
+    constexpr int n = decltype(N)::value;
+    constexpr int s = n / 16, i = n % 16;
+    constexpr int mt = i >> 2, nt = i & 3;
+    constexpr char kind = kFwd ? kPlanFwd[n] : kPlanDgrad[n];
+    acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+        __builtin_bit_cast(bf16x8, b[s & 1][nt]), __builtin_bit_cast(bf16x8, a[s & 1][mt]),
+        acc[mt][nt], 0, 0, 0);
+    if constexpr (kind == 'R' || kind == 'n') {
+      read_frag(Acur, Bcur, a, b, s + 1, 2 * i, (s + 1) & 1, jl, grp);
+      read_frag(Acur, Bcur, a, b, s + 1, 2 * i + 1, (s + 1) & 1, jl, grp);
+    }
+    if constexpr (kind == 'N' || kind == 'n')
+      dma(Aoth, 8 + plan_index(kFwd ? kPlanFwd : kPlanDgrad, n, 'N'), t1);
+    if constexpr (kind == 'A') {
+      constexpr int d = plan_index(kFwd ? kPlanFwd : kPlanDgrad, n, 'A');
+      // The wave's reads of Acur (sub-step 3's fragments) have returned.
+      if constexpr (d == 0) __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+      dma(Acur, d, t2);
+    }
+    if constexpr (kind == 'L') {
+      // One half-quarter of the product table.  Pinning the absmax here
+      // keeps the (pure) arithmetic at its slot.
+      constexpr int h = plan_index(kFwd ? kPlanFwd : kPlanDgrad, n, 'L');
+      float am = ta;
+      pin(am);
+      make_lut_half<false>(am, h, lutd, lut);
+    }
+    if constexpr (kind == 'W') {
+      constexpr int j = plan_index(kFwd ? kPlanFwd : kPlanDgrad, n, 'W');
+      constexpr int k = j / kWordStages, stage = j % kWordStages;
+      // Each stage pins its inputs at its slot (see above).
+      if constexpr (stage == 0) {
+        uint32_t w = words[k];
+        pin(w);
+        word_select_idx(w, wl);
+      } else if constexpr (stage == 1) {
+        uint32_t w = words[k];
+        pin(w);
+        word_select_mask(w, wl);
+      } else if constexpr (stage == 2) {
+        pin(wl.selE);
+        pin(wl.maskE);
+        word_even(lut, wl);
+      } else if constexpr (stage == 3) {
+        pin(wl.selO);
+        pin(wl.maskO);
+        word_odd(lut, wl);
+      } else if constexpr (stage == 4) {
+        pin(wl.loE);
+        pin(wl.hiE);
+        pin(wl.loO);
+        pin(wl.hiO);
+        word_pairs(wl, wp[k]);
+      } else {
+        uint32_t o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) pin(wp[k][e]);
+        pairs_merge(wp[k], o);
+        prod.template store<kPar, k, 0>(Bnext, o);
+      }
+    }
+    if constexpr (!kFwd && dgrad_p_slot(n)) {
+      constexpr int j = p_index(n);
+      constexpr int k = j >> 1, half = j & 1;
+      prod.template store<kPar, k, 2 * half>(Bnext, wp[k]);
+      prod.template store<kPar, k, 2 * half + 1>(Bnext, wp[k]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  });
+  step_barrier();
+}
+
+// The last step's final 8 MFMAs (see gemm_step).
 __device__ __forceinline__ void gemm_tail(floatx16 (&acc)[4][4], const u32x4 (&a)[2][4],
                                           const u32x4 (&b)[2][4]) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-    acc[3][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-        __builtin_bit_cast(bf16x8, b[1][i]), __builtin_bit_cast(bf16x8, a[1][3]), acc[3][i], 0,
-        0, 0);
+  for (int i = 0; i < 8; ++i) {
+    const int mt = 2 + (i >> 2), nt = i & 3;
+    acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+        __builtin_bit_cast(bf16x8, b[1][nt]), __builtin_bit_cast(bf16x8, a[1][mt]), acc[mt][nt],
+        0, 0, 0);
+  }
+}
+
+// Prologue, main loop and tail of the GEMM.  The LDS buffers come in as
+// distinct __restrict__ pointers: the compiler then knows that the
+// activation DMAs into one buffer never alias the fragment reads of the
+// other, and waits (vmcnt) only for the DMAs whose buffer a read touches.
+template <class Producer>
+__device__ __forceinline__ void gemm_main(const GemmArgs &g, const Producer &prod,
+                                          floatx16 (&acc)[4][4], u32x4 *__restrict__ A0,
+                                          u32x4 *__restrict__ A1, u32x4 *__restrict__ B0,
+                                          u32x4 *__restrict__ B1, __amdgpu_buffer_rsrc_t arsrc,
+                                          const uint32_t (&aoff)[16], int64_t nsteps, int jl,
+                                          int grp) {
+  // Prologue: packed weights of steps 0 and 1, the activation tile of step 0
+  // and rows 0-63 of step 1 (DMA), then the weight tile of step 0
+  // dequantized into B0.  The fences fix the order of issue, so that
+  // vmcnt(8) at the barrier means "all but step 1's 8 DMAs" to the compiler
+  // as to the hardware.
+  u32x4 wc, wn;
+  AbsRaw ac, an;
+  {
+    u32x4 w0;
+    AbsRaw s0;
+    prod.load(g, 0, w0, s0);
+    prod.load(g, nsteps > 1 ? 1 : 0, wc, ac);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(arsrc, (lds_void_t *)(A0 + i * 64), 16,
+                                               (int)aoff[i], 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    const int step1 = (nsteps > 1) ? kStep * 2 : 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(arsrc, (lds_void_t *)(A1 + i * 64), 16,
+                                               (int)aoff[i], step1, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    prod.store(B0, w0, s0);
+  }
+  step_barrier();
+
+  // Fragment registers; the first step's head multiplies zeros.
+  u32x4 fa[2][4], fb[2][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    fa[1][i] = (u32x4){0u, 0u, 0u, 0u};
+    fb[1][i] = (u32x4){0u, 0u, 0u, 0u};
+  }
+
+  // Two steps per iteration, even then odd buffers; the packed-weight
+  // registers swap roles instead of being copied.  The last steps' look-ahead
+  // work reads clamped (valid) addresses and fills buffers nobody reads
+  // again.
+#pragma unroll 1
+  for (int64_t t = 0; t + 1 < nsteps; t += 2) {
+    gemm_step<Producer, 1>(g, prod, acc, fa, fb, A0, A1, B0, B1, arsrc, aoff, wc, ac,
+                        wn, an, t, nsteps, jl, grp);
+    gemm_step<Producer, 0>(g, prod, acc, fa, fb, A1, A0, B1, B0, arsrc, aoff, wn, an,
+                        wc, ac, t + 1, nsteps, jl, grp);
+  }
+  if (nsteps & 1)
+    gemm_step<Producer, 1>(g, prod, acc, fa, fb, A0, A1, B0, B1, arsrc, aoff, wc, ac,
+                        wn, an, nsteps - 1, nsteps, jl, grp);
+  gemm_tail(acc, fa, fb);
+  // No LDS DMA may still be in flight when the workgroup's LDS is released.
+  __builtin_amdgcn_s_waitcnt(0);
 }
 
 template <class Producer>
@@ -375,7 +584,7 @@ __global__ void __launch_bounds__(kGemmThreads, 1) nf4_gemm_kernel(const GemmArg
 
   // Direct-to-LDS activation loads: instruction i writes rows 8i..8i+7 of the
   // wave's 128-row tile as 1 KB, lane p at LDS unit 64i + p, i.e. row
-  // 8i + p/8, physical unit p%8, which holds logical unit (p%8) ^ (row%8)
+  // 8i + p/8, physical unit p%8, which holds logical unit (p%8) ^ swz(row)
   // (the swizzle of lds_unit).  aoff[i] is lane p's byte offset from the
   // wave's first (clamped) row at k = 0; rows beyond M are clamped.  The
   // loads go through a buffer resource based at that row, with the step's
@@ -396,12 +605,12 @@ __global__ void __launch_bounds__(kGemmThreads, 1) nf4_gemm_kernel(const GemmArg
     const int rr = 8 * i + (lane >> 3);
     int rel = rr + skip;
     if (rel > avail - 1) rel = avail - 1;
-    const int u = (lane & 7) ^ (rr & 7);
+    const int u = (lane & 7) ^ swz(rr);
     aoff[i] = (uint32_t)rel * lda2 + 16u * (uint32_t)u;
   }
 
   Producer prod;
-  prod.init(g, o0);
+  prod.init(g, o0, (uint32_t)(uintptr_t)(lds_void_t *)&g_lds_b[0][0]);
 
   floatx16 acc[4][4];
 #pragma unroll
@@ -411,58 +620,8 @@ __global__ void __launch_bounds__(kGemmThreads, 1) nf4_gemm_kernel(const GemmArg
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[mt][nt][v] = 0.0f;
 
-  u32x4 *a0w = &g_lds_a[wave][0][0];
-  u32x4 *a1w = &g_lds_a[wave][1][0];
-
-  // Prologue: activation tile of step 0 (DMA), weight tile of step 0
-  // (dequantized into b0), packed weights of step 1 in registers.
-#pragma unroll
-  for (int i = 0; i < 16; ++i)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(arsrc, (lds_void_t *)(a0w + i * 64), 16, (int)aoff[i],
-                                             0, 0, 0);
-  {
-    u32x4 w0;
-    AbsRaw s0;
-    prod.load(g, 0, w0, s0);
-    prod.store(g_lds_b[0], w0, s0);
-  }
-  u32x4 wc, wn;
-  AbsRaw ac, an;
-  prod.load(g, nsteps > 1 ? 1 : 0, wc, ac);
-  __builtin_amdgcn_s_waitcnt(0);  // the DMA of step 0 has landed in LDS
-  __syncthreads();
-
-  // Fragment registers; the first step's tail multiplies zeros.
-  u32x4 fa[2][4], fb[2][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    fa[1][i] = (u32x4){0u, 0u, 0u, 0u};
-    fb[1][i] = (u32x4){0u, 0u, 0u, 0u};
-  }
-
-  // Two steps per iteration, even then odd buffers; the packed-weight
-  // registers swap roles instead of being copied.  After each step the next
-  // step's activation tile (direct-to-LDS) and weight tile are complete.
-  // The last step's "next" work reads clamped (valid) addresses and fills
-  // buffers nobody reads again.
-#pragma unroll 1
-  for (int64_t t = 0; t + 1 < nsteps; t += 2) {
-    gemm_step<Producer>(g, prod, acc, fa, fb, a0w, a1w, g_lds_b[0], g_lds_b[1], arsrc, aoff, wc,
-                        ac, wn, an, t, nsteps, jl, grp);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    gemm_step<Producer>(g, prod, acc, fa, fb, a1w, a0w, g_lds_b[1], g_lds_b[0], arsrc, aoff, wn,
-                        an, wc, ac, t + 1, nsteps, jl, grp);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-  }
-  if (nsteps & 1) {
-    gemm_step<Producer>(g, prod, acc, fa, fb, a0w, a1w, g_lds_b[0], g_lds_b[1], arsrc, aoff, wc,
-                        ac, wn, an, nsteps - 1, nsteps, jl, grp);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-  }
-  gemm_tail(acc, fa, fb);
+  gemm_main<Producer>(g, prod, acc, &g_lds_a[wave][0][0], &g_lds_a[wave][1][0], g_lds_b[0],
+                      g_lds_b[1], arsrc, aoff, nsteps, jl, grp);
 
   // Epilogue: fp32 -> bf16 (RNE).  The MFMAs take the weight fragment as
   // their first operand, so each accumulator tile is the transposed output
