@@ -26,6 +26,8 @@
 // accumulator layout is lane l: column l % 32, row 8(v/4) + 4g + v%4; the
 // weight fragment is the first operand, so the accumulator's columns are
 // activation rows and its rows are output columns.
+#include <type_traits>
+
 #include "abi_common.hpp"
 #include "nf4_device.hpp"
 
@@ -84,17 +86,6 @@ __device__ __forceinline__ int lds_unit_b(int row, int u) {
   return row * 8 + (u ^ swz(row) ^ ((row >> 4) & 6));
 }
 
-// Lookup of packed word w with product table t, finished by the producer's
-// merge.
-template <class Producer>
-__device__ __forceinline__ void dequant_word(const Lut16 &t, uint32_t w, uint32_t out[4]) {
-  WordLookup x;
-  word_select(w, x);
-  word_even(t, x);
-  word_odd(t, x);
-  Producer::merge(x, out);
-}
-
 // Absmax of block `blk`: fp32, or the double-quant code times its group
 // scale.  It is loaded as raw words and decoded a step later, so that the
 // loads' latency never stalls the wave.  A template flag rather than a
@@ -122,33 +113,69 @@ __device__ __forceinline__ float absmax_value(const AbsRaw &r) {
   return kDQ ? (float)r.q * r.s : r.s;
 }
 
+// Producer interface used by the GEMM step (phase = step index mod kUnroll):
+//   prologue_load / prologue_store   loads for steps 0 and 1; step 0's tile
+//   issue_loads<phase>(g, t, nsteps) loads issued in step t for later steps
+//   prepare<phase>()                 register work once those loads landed
+//   word<phase>(k), table_absmax<phase>()
+//                                    packed word k and absmax of step t+1,
+//                                    the tile dequantized during step t
+//   finish<phase>()                  end of step t
+//   store<kPar, k, part>(lds, out)   writes the dequantized word k.
+//
+// Per-step loading (PerStepLoads): step t loads the packed words and raw
+// absmax of step t+2 into register set t & 1; step t+1's tile comes from the
+// other set, loaded a step earlier.
+template <bool kDQ, class Derived>
+struct PerStepLoads {
+  static constexpr int kUnroll = 2;
+  u32x4 w[2];
+  AbsRaw a[2];
+  u32x4 w0;  // step 0 (prologue)
+  AbsRaw a0;
+  __device__ __forceinline__ void prologue_load(const GemmArgs &g, int64_t nsteps) {
+    const Derived &d = static_cast<const Derived &>(*this);
+    d.load_step(g, 0, w0, a0);
+    d.load_step(g, nsteps > 1 ? 1 : 0, w[1], a[1]);
+  }
+  template <int kPhase>
+  __device__ __forceinline__ void issue_loads(const GemmArgs &g, int64_t t, int64_t nsteps) {
+    const int64_t t2 = (t + 2 < nsteps) ? t + 2 : nsteps - 1;
+    static_cast<const Derived &>(*this).load_step(g, t2, w[kPhase & 1], a[kPhase & 1]);
+  }
+  template <int kPhase>
+  __device__ __forceinline__ void prepare() {}
+  template <int kPhase>
+  __device__ __forceinline__ void finish() {}
+  template <int kPhase>
+  __device__ __forceinline__ uint32_t word(int k) const {
+    return w[(kPhase + 1) & 1][k];
+  }
+  template <int kPhase>
+  __device__ __forceinline__ float table_absmax() const {
+    return static_cast<const Derived &>(*this).masked(absmax_value<kDQ>(a[(kPhase + 1) & 1]));
+  }
+  __device__ __forceinline__ void prologue_store(u32x4 *lds) const {
+    const Derived &d = static_cast<const Derived &>(*this);
+    d.store_tile(lds, w0, d.masked(absmax_value<kDQ>(a0)));
+  }
+};
+
 // Forward producer: thread -> (row n_local, half h), 32 consecutive k of one
 // block; writes 4 swizzled 16-B units of its row.  Lanes 16j..16j+15 of a
 // wave take 16 consecutive rows at one half, so each 16-lane group of a
 // ds_write_b128 covers 16 rows at one logical unit (no bank conflicts).
-template <bool kDQ>
-struct FwdProducer {
-  const uint8_t *ptr;   // packed bytes of (row, half) at step 0
-  int64_t am_idx;       // absmax block index at step 0
+// FwdStore holds that mapping and the stores; the two forward producers
+// differ only in how the packed words and absmax reach the registers.
+struct FwdStore {
+  static constexpr bool kFwd = true;
   int row, h;
-  __device__ void init(const GemmArgs &g, int64_t o0, uint32_t b0_lds) {
-    (void)b0_lds;
+  __device__ __forceinline__ void init_row() {
     const int lane = threadIdx.x & 63;
     row = 32 * (threadIdx.x >> 6) + 16 * (lane >> 5) + (lane & 15);
     h = (lane >> 4) & 1;
-    int64_t n = o0 + row;
-    if (n >= g.wn) n = g.wn - 1;  // ragged N: clamp (outputs are not stored)
-    ptr = g.packed + n * (g.wk >> 1) + 16 * h;
-    am_idx = n * (g.wk >> 6);
   }
-  __device__ __forceinline__ void load(const GemmArgs &g, int64_t step, u32x4 &w, AbsRaw &a) const {
-    w = *reinterpret_cast<const u32x4 *>(ptr + step * 32);
-    a = absmax_load<kDQ>(g.am, am_idx + step);
-  }
-  // The absmax the product table is built from.
-  __device__ __forceinline__ float table_absmax(const AbsRaw &a) const {
-    return absmax_value<kDQ>(a);
-  }
+  __device__ __forceinline__ float masked(float a) const { return a; }
   // The 8 elements of a word in natural order: out[j] = elements 2j, 2j+1.
   static __device__ __forceinline__ void merge(const WordLookup &x, uint32_t out[4]) {
     word_merge(x, out);
@@ -163,15 +190,159 @@ struct FwdProducer {
     lds[lds_unit_b(row, 4 * h + k)] = v;
   }
   // Whole-tile store (prologue).
-  __device__ __forceinline__ void store(u32x4 *lds, const u32x4 &w, const AbsRaw &a) const {
-    const Lut16 lut = make_lut<false>(table_absmax(a));
+  __device__ __forceinline__ void store_tile(u32x4 *lds, const u32x4 &w, float am) const {
+    const Lut16 lut = make_lut<false>(am);
     const uint32_t words[4] = {w.x, w.y, w.z, w.w};
     static_for<0, 4>([&](auto K) {
       constexpr int k = decltype(K)::value;
       uint32_t o[4];
-      dequant_word<FwdProducer>(lut, words[k], o);
+      WordLookup x;
+      word_select(words[k], x);
+      word_even(lut, x);
+      word_odd(lut, x);
+      word_merge(x, o);
       this->template store<0, k, 0>(lds, o);
     });
+  }
+};
+
+// Forward producer with one load per step and thread (any k % 64 == 0).
+template <bool kDQ>
+struct FwdProducer : FwdStore, PerStepLoads<kDQ, FwdProducer<kDQ>> {
+  const uint8_t *ptr;   // packed bytes of (row, half) at step 0
+  int64_t am_idx;       // absmax block index at step 0
+  __device__ void init(const GemmArgs &g, int64_t o0, uint32_t b0_lds) {
+    (void)b0_lds;
+    init_row();
+    int64_t n = o0 + row;
+    if (n >= g.wn) n = g.wn - 1;  // ragged N: clamp (outputs are not stored)
+    ptr = g.packed + n * (g.wk >> 1) + 16 * h;
+    am_idx = n * (g.wk >> 6);
+  }
+  __device__ __forceinline__ void load_step(const GemmArgs &g, int64_t step, u32x4 &w,
+                                            AbsRaw &a) const {
+    w = *reinterpret_cast<const u32x4 *>(ptr + step * 32);
+    a = absmax_load<kDQ>(g.am, am_idx + step);
+  }
+};
+
+// Forward producer with batched loads (k % 256 == 0, 4-step unroll).  A
+// thread's per-step data (16 B of packed nibbles, one absmax) sits in a
+// different cache line for each of the wave's 32 rows, and the activation
+// stream evicts those lines before the next step comes back to them.  So:
+//  * packed nibbles are loaded two steps at a time: instruction X covers the
+//    wave's rows 0-15 and instruction Y rows 16-31, 64 contiguous bytes per
+//    row (lane l: row l % 16, 16-B chunk l / 16 = (step 2p + c / 2, half
+//    c % 2)).  v_permlane32_swap then exchanges X's upper 32 lanes with Y's
+//    lower 32: X holds step 2p and Y step 2p+1, both in the thread -> (row,
+//    half) layout of FwdStore.  Half the cache lines per step.
+//  * absmax is loaded four steps at a time: one dword of double-quant codes
+//    (or one float4 of fp32 absmax) plus one scale per thread.  The four
+//    blocks lie in one scale group (dq_group >= 4, and 4 | blocks per row).
+// Registers: pair set 0 is loaded in phase 0 (steps t+2, t+3), pair set 1 in
+// phase 2; the absmax of group t/4 + 1 in phase 0.
+template <bool kDQ>
+struct FwdBatchProducer : FwdStore {
+  static constexpr int kUnroll = 4;
+  const uint8_t *pkx, *pky;  // pair loads of instructions X and Y at pair 0
+  int64_t am_idx;            // absmax block index of (row) at step 0
+  int64_t npairs, ngroups;
+  u32x4 X[2], Y[2];
+  typedef typename std::conditional<kDQ, u32x2, u32x4>::type Group;
+  Group cur, nxt;  // kDQ: {codes of 4 blocks, scale bits}; else 4 fp32 absmax
+
+  __device__ void init(const GemmArgs &g, int64_t o0, uint32_t b0_lds) {
+    (void)b0_lds;
+    init_row();
+    const int lane = threadIdx.x & 63;
+    int64_t n = o0 + row;
+    if (n >= g.wn) n = g.wn - 1;
+    am_idx = n * (g.wk >> 6);
+    int64_t nx = o0 + 32 * (threadIdx.x >> 6) + (lane & 15);
+    int64_t ny = nx + 16;
+    if (nx >= g.wn) nx = g.wn - 1;
+    if (ny >= g.wn) ny = g.wn - 1;
+    pkx = g.packed + nx * (g.wk >> 1) + 16 * (lane >> 4);
+    pky = g.packed + ny * (g.wk >> 1) + 16 * (lane >> 4);
+    npairs = g.R >> 7;
+    ngroups = g.R >> 8;
+  }
+  __device__ __forceinline__ void load_pair(int64_t p, u32x4 &x, u32x4 &y) const {
+    x = *reinterpret_cast<const u32x4 *>(pkx + p * 64);
+    y = *reinterpret_cast<const u32x4 *>(pky + p * 64);
+  }
+  __device__ __forceinline__ void load_group(const GemmArgs &g, int64_t gi, Group &v) const {
+    const int64_t blk = am_idx + 4 * gi;
+    if constexpr (kDQ) {
+      v.x = *reinterpret_cast<const uint32_t *>(g.am.q + blk);
+      v.y = __builtin_bit_cast(uint32_t, g.am.scale[blk >> g.am.group_shift]);
+    } else {
+      v = *reinterpret_cast<const u32x4 *>(g.am.absmax + blk);
+    }
+  }
+  // The vector elements are copied to scalars before the bit casts:
+  // __builtin_bit_cast of an ext_vector element expression reads element 0.
+  template <int b>
+  static __device__ __forceinline__ float group_absmax(const Group &v) {
+    if constexpr (kDQ) {
+      const uint32_t q = v.x, s = v.y;
+      return (float)((q >> (8 * b)) & 0xffu) * __builtin_bit_cast(float, s);
+    } else {
+      const uint32_t a = v[b];
+      return __builtin_bit_cast(float, a);
+    }
+  }
+  static __device__ __forceinline__ void swap(u32x4 &x, u32x4 &y) {
+    static_for<0, 4>([&](auto I) {
+      constexpr int i = decltype(I)::value;
+      const auto r = __builtin_amdgcn_permlane32_swap(x[i], y[i], false, false);
+      x[i] = r[0];
+      y[i] = r[1];
+    });
+  }
+  __device__ __forceinline__ void prologue_load(const GemmArgs &g, int64_t nsteps) {
+    (void)nsteps;
+    load_pair(0, X[1], Y[1]);
+    load_group(g, 0, cur);
+  }
+  __device__ __forceinline__ void prologue_store(u32x4 *lds) {
+    swap(X[1], Y[1]);
+    store_tile(lds, X[1], group_absmax<0>(cur));
+  }
+  template <int kPhase>
+  __device__ __forceinline__ void issue_loads(const GemmArgs &g, int64_t t, int64_t nsteps) {
+    (void)nsteps;
+    if constexpr (kPhase == 0 || kPhase == 2) {
+      int64_t p = (t + 2) >> 1;
+      if (p > npairs - 1) p = npairs - 1;  // look-ahead past the end: unused
+      load_pair(p, X[kPhase >> 1], Y[kPhase >> 1]);
+    }
+    if constexpr (kPhase == 0) {
+      int64_t gi = (t >> 2) + 1;
+      if (gi > ngroups - 1) gi = ngroups - 1;
+      load_group(g, gi, nxt);
+    }
+  }
+  template <int kPhase>
+  __device__ __forceinline__ void prepare() {
+    if constexpr (kPhase == 1) swap(X[0], Y[0]);
+    if constexpr (kPhase == 3) swap(X[1], Y[1]);
+  }
+  template <int kPhase>
+  __device__ __forceinline__ uint32_t word(int k) const {
+    if constexpr (kPhase == 0) return Y[1][k];
+    else if constexpr (kPhase == 1) return X[0][k];
+    else if constexpr (kPhase == 2) return Y[0][k];
+    else return X[1][k];
+  }
+  template <int kPhase>
+  __device__ __forceinline__ float table_absmax() const {
+    if constexpr (kPhase == 3) return group_absmax<0>(nxt);
+    else return group_absmax<kPhase + 1>(cur);
+  }
+  template <int kPhase>
+  __device__ __forceinline__ void finish() {
+    if constexpr (kPhase == 3) cur = nxt;
   }
 };
 
@@ -191,7 +362,8 @@ struct FwdProducer {
 // would wait for those, vmcnt(0), before every store).  Their completion is
 // covered by the explicit lgkmcnt(0) before each step's barrier.
 template <bool kDQ>
-struct DgradProducer {
+struct DgradProducer : PerStepLoads<kDQ, DgradProducer<kDQ>> {
+  static constexpr bool kFwd = false;
   const uint8_t *ptr;
   int64_t am_idx;
   int r, q;
@@ -211,14 +383,15 @@ struct DgradProducer {
     ptr = g.packed + (int64_t)r * (g.wk >> 1) + (c >> 1);
     am_idx = (int64_t)r * (g.wk >> 6) + (c >> 6);
   }
-  __device__ __forceinline__ void load(const GemmArgs &g, int64_t step, u32x4 &w, AbsRaw &a) const {
+  __device__ __forceinline__ void load_step(const GemmArgs &g, int64_t step, u32x4 &w,
+                                            AbsRaw &a) const {
     // Step s covers W rows 64s .. 64s+63.
     w = *reinterpret_cast<const u32x4 *>(ptr + step * 64 * (g.wk >> 1));
     a = absmax_load<kDQ>(g.am, am_idx + step * 64 * (g.wk >> 6));
   }
   // Columns beyond k read column 0's bytes and are zeroed via the absmax.
-  __device__ __forceinline__ float table_absmax(const AbsRaw &a) const {
-    return __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, absmax_value<kDQ>(a)) & valid_mask);
+  __device__ __forceinline__ float masked(float a) const {
+    return __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, a) & valid_mask);
   }
   // Elements are stored one by one, so the pairs of the first merge half
   // suffice: element j is half (j >> 1) & 1 of out[(j & 1) + 2 * (j >> 2)].
@@ -243,13 +416,17 @@ struct DgradProducer {
         asm volatile("ds_write_b16_d16_hi %0, %1 offset:%2" ::"v"(a), "v"(pr), "i"(off) : "memory");
     });
   }
-  __device__ __forceinline__ void store(u32x4 *lds, const u32x4 &w, const AbsRaw &a) const {
-    const Lut16 lut = make_lut<false>(table_absmax(a));
+  __device__ __forceinline__ void store_tile(u32x4 *lds, const u32x4 &w, float am) const {
+    const Lut16 lut = make_lut<false>(am);
     const uint32_t words[4] = {w.x, w.y, w.z, w.w};
     static_for<0, 4>([&](auto K) {
       constexpr int k = decltype(K)::value;
       uint32_t o[4];
-      dequant_word<DgradProducer>(lut, words[k], o);
+      WordLookup x;
+      word_select(words[k], x);
+      word_even(lut, x);
+      word_odd(lut, x);
+      word_pairs(x, o);
       this->template store<0, k, 0>(lds, o);
       this->template store<0, k, 1>(lds, o);
       this->template store<0, k, 2>(lds, o);
@@ -370,8 +547,8 @@ constexpr int p_index(int n) {
 // One 64-deep reduction step t: 4 sub-steps of 16 MFMAs over the activation
 // tile in Acur (this wave's 128 rows) and the weight tile in Bcur.  Alongside
 // the MFMAs it reads the next sub-step's fragments, dequantizes step t+1's
-// packed weights (wc, ac, loaded a step ago) into Bnext, loads the packed
-// weights of step t+2 (wn_, an_) and moves activation rows into LDS with
+// packed weights (loaded by the producer in an earlier step) into Bnext,
+// issues the producer's loads for later steps and moves activation rows into LDS with
 // direct-to-LDS loads (1 KB = 8 whole 128-B rows per instruction): rows
 // 64-127 of step t+1 into Aoth (read last in step t-1) and rows 0-63 of step
 // t+2 into Acur after this wave's last reads of it.  Every DMA has at least
@@ -384,19 +561,18 @@ constexpr int p_index(int n) {
 // (a[1][2..3] x b[1][0..3], operands already in registers) open the NEXT
 // call, after the barrier, each followed by one fragment read of the new
 // step's sub-step 0.  The first call runs them on zero operands.
-template <class Producer, int kPar>
-__device__ __forceinline__ void gemm_step(const GemmArgs &g, const Producer &prod,
+template <class Producer, int kPhase>
+__device__ __forceinline__ void gemm_step(const GemmArgs &g, Producer &prod,
                                           floatx16 (&acc)[4][4], u32x4 (&a)[2][4],
                                           u32x4 (&b)[2][4], u32x4 *Acur, u32x4 *Aoth,
                                           const u32x4 *Bcur, u32x4 *Bnext,
                                           __amdgpu_buffer_rsrc_t arsrc, const uint32_t (&aoff)[16],
-                                          const u32x4 &wc, const AbsRaw &ac, u32x4 &wn_, AbsRaw &an_,
                                           int64_t t, int64_t nsteps, int jl, int grp) {
-  constexpr bool kFwd = Producer::kStoreParts == 1;
+  constexpr int kPar = 1 - (kPhase & 1);
+  constexpr bool kFwd = Producer::kFwd;
   constexpr int kWordStages = kFwd ? 6 : 5;
   const int64_t t1 = (t + 1 < nsteps) ? t + 1 : nsteps - 1;
   const int64_t t2 = (t + 2 < nsteps) ? t + 2 : nsteps - 1;
-  const uint32_t words[4] = {wc.x, wc.y, wc.z, wc.w};
   Lut16 lut;
   uint32_t lutd[2];
   WordLookup wl;
@@ -415,8 +591,9 @@ __device__ __forceinline__ void gemm_step(const GemmArgs &g, const Producer &pro
         __builtin_bit_cast(bf16x8, b[1][nt]), __builtin_bit_cast(bf16x8, a[1][mt]),
         acc[mt][nt], 0, 0, 0);
     read_frag(Acur, Bcur, a, b, 0, i, 0, jl, grp);
-    if constexpr (i == 3) prod.load(g, t2, wn_, an_);
-    if constexpr (i == 6) ta = prod.table_absmax(ac);
+    if constexpr (i == 3) prod.template issue_loads<kPhase>(g, t, nsteps);
+    if constexpr (i == 5) prod.template prepare<kPhase>();
+    if constexpr (i == 6) ta = prod.template table_absmax<kPhase>();
     __builtin_amdgcn_sched_barrier(0);
   });
   static_for<0, 56>([&](auto N) {
@@ -452,11 +629,11 @@ __device__ __forceinline__ void gemm_step(const GemmArgs &g, const Producer &pro
       constexpr int k = j / kWordStages, stage = j % kWordStages;
       // Each stage pins its inputs at its slot (see above).
       if constexpr (stage == 0) {
-        uint32_t w = words[k];
+        uint32_t w = prod.template word<kPhase>(k);
         pin(w);
         word_select_idx(w, wl);
       } else if constexpr (stage == 1) {
-        uint32_t w = words[k];
+        uint32_t w = prod.template word<kPhase>(k);
         pin(w);
         word_select_mask(w, wl);
       } else if constexpr (stage == 2) {
@@ -490,6 +667,7 @@ __device__ __forceinline__ void gemm_step(const GemmArgs &g, const Producer &pro
     __builtin_amdgcn_sched_barrier(0);
   });
   step_barrier();
+  prod.template finish<kPhase>();
 }
 
 // The last step's final 8 MFMAs (see gemm_step).
@@ -509,38 +687,31 @@ __device__ __forceinline__ void gemm_tail(floatx16 (&acc)[4][4], const u32x4 (&a
 // activation DMAs into one buffer never alias the fragment reads of the
 // other, and waits (vmcnt) only for the DMAs whose buffer a read touches.
 template <class Producer>
-__device__ __forceinline__ void gemm_main(const GemmArgs &g, const Producer &prod,
+__device__ __forceinline__ void gemm_main(const GemmArgs &g, Producer &prod,
                                           floatx16 (&acc)[4][4], u32x4 *__restrict__ A0,
                                           u32x4 *__restrict__ A1, u32x4 *__restrict__ B0,
                                           u32x4 *__restrict__ B1, __amdgpu_buffer_rsrc_t arsrc,
                                           const uint32_t (&aoff)[16], int64_t nsteps, int jl,
                                           int grp) {
-  // Prologue: packed weights of steps 0 and 1, the activation tile of step 0
-  // and rows 0-63 of step 1 (DMA), then the weight tile of step 0
+  // Prologue: the producer's loads for steps 0 and 1, the activation tile of
+  // step 0 and rows 0-63 of step 1 (DMA), then the weight tile of step 0
   // dequantized into B0.  The fences fix the order of issue, so that
   // vmcnt(8) at the barrier means "all but step 1's 8 DMAs" to the compiler
   // as to the hardware.
-  u32x4 wc, wn;
-  AbsRaw ac, an;
-  {
-    u32x4 w0;
-    AbsRaw s0;
-    prod.load(g, 0, w0, s0);
-    prod.load(g, nsteps > 1 ? 1 : 0, wc, ac);
-    __builtin_amdgcn_sched_barrier(0);
+  prod.prologue_load(g, nsteps);
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int i = 0; i < 16; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(arsrc, (lds_void_t *)(A0 + i * 64), 16,
-                                               (int)aoff[i], 0, 0, 0);
-    __builtin_amdgcn_sched_barrier(0);
-    const int step1 = (nsteps > 1) ? kStep * 2 : 0;
+  for (int i = 0; i < 16; ++i)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(arsrc, (lds_void_t *)(A0 + i * 64), 16,
+                                             (int)aoff[i], 0, 0, 0);
+  __builtin_amdgcn_sched_barrier(0);
+  const int step1 = (nsteps > 1) ? kStep * 2 : 0;
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(arsrc, (lds_void_t *)(A1 + i * 64), 16,
-                                               (int)aoff[i], step1, 0, 0);
-    __builtin_amdgcn_sched_barrier(0);
-    prod.store(B0, w0, s0);
-  }
+  for (int i = 0; i < 8; ++i)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(arsrc, (lds_void_t *)(A1 + i * 64), 16,
+                                             (int)aoff[i], step1, 0, 0);
+  __builtin_amdgcn_sched_barrier(0);
+  prod.prologue_store(B0);
   step_barrier();
 
   // Fragment registers; the first step's head multiplies zeros.
@@ -551,20 +722,31 @@ __device__ __forceinline__ void gemm_main(const GemmArgs &g, const Producer &pro
     fb[1][i] = (u32x4){0u, 0u, 0u, 0u};
   }
 
-  // Two steps per iteration, even then odd buffers; the packed-weight
-  // registers swap roles instead of being copied.  The last steps' look-ahead
-  // work reads clamped (valid) addresses and fills buffers nobody reads
-  // again.
+  // kUnroll steps per iteration; even phases use the even buffers (A0, B0
+  // read, B1 written), odd phases the odd ones, so no register or pointer is
+  // copied between steps.  The last steps' look-ahead work reads clamped
+  // (valid) addresses and fills buffers nobody reads again.  A producer
+  // with kUnroll 4 needs nsteps % 4 == 0 (checked at launch); with kUnroll 2
+  // an odd last step runs alone.
+  constexpr int U = Producer::kUnroll;
+  int64_t t = 0;
 #pragma unroll 1
-  for (int64_t t = 0; t + 1 < nsteps; t += 2) {
-    gemm_step<Producer, 1>(g, prod, acc, fa, fb, A0, A1, B0, B1, arsrc, aoff, wc, ac,
-                        wn, an, t, nsteps, jl, grp);
-    gemm_step<Producer, 0>(g, prod, acc, fa, fb, A1, A0, B1, B0, arsrc, aoff, wn, an,
-                        wc, ac, t + 1, nsteps, jl, grp);
+  for (; t + U <= nsteps; t += U) {
+    static_for<0, U>([&](auto P) {
+      constexpr int p = decltype(P)::value;
+      if constexpr ((p & 1) == 0)
+        gemm_step<Producer, p>(g, prod, acc, fa, fb, A0, A1, B0, B1, arsrc, aoff, t + p, nsteps,
+                               jl, grp);
+      else
+        gemm_step<Producer, p>(g, prod, acc, fa, fb, A1, A0, B1, B0, arsrc, aoff, t + p, nsteps,
+                               jl, grp);
+    });
   }
-  if (nsteps & 1)
-    gemm_step<Producer, 1>(g, prod, acc, fa, fb, A0, A1, B0, B1, arsrc, aoff, wc, ac,
-                        wn, an, nsteps - 1, nsteps, jl, grp);
+  if constexpr (U == 2) {
+    if (t < nsteps)
+      gemm_step<Producer, 0>(g, prod, acc, fa, fb, A0, A1, B0, B1, arsrc, aoff, t, nsteps, jl,
+                             grp);
+  }
   gemm_tail(acc, fa, fb);
   // No LDS DMA may still be in flight when the workgroup's LDS is released.
   __builtin_amdgcn_s_waitcnt(0);
@@ -730,8 +912,16 @@ int32_t nf4s_gemm_fwd(const uint16_t *x, const nf4s_tensor *w, int64_t m, int64_
   g.wn = n;
   g.tiles_m = (int32_t)((m + kTileM - 1) / kTileM);
   g.tiles_o = (int32_t)((n + kTileO - 1) / kTileO);
-  if (w->absmax_q != nullptr)
-    return launch_gemm<FwdProducer<true>>(g, as_stream(stream), "nf4_gemm_fwd");
+  // Batched weight loads need whole 4-block absmax groups per row (k % 256),
+  // aligned group loads, and 4-block groups inside one double-quant scale.
+  const bool dq = w->absmax_q != nullptr;
+  const bool batch = (k % 256 == 0) &&
+                     (dq ? (aligned(w->absmax_q, 4) && w->dq_group >= 4)
+                         : aligned(w->absmax, 16));
+  if (batch)
+    return dq ? launch_gemm<FwdBatchProducer<true>>(g, as_stream(stream), "nf4_gemm_fwd")
+              : launch_gemm<FwdBatchProducer<false>>(g, as_stream(stream), "nf4_gemm_fwd");
+  if (dq) return launch_gemm<FwdProducer<true>>(g, as_stream(stream), "nf4_gemm_fwd");
   return launch_gemm<FwdProducer<false>>(g, as_stream(stream), "nf4_gemm_fwd");
 }
 

@@ -69,6 +69,53 @@ def test_fwd_small_vs_oracle(m, n, k, dq):
     assert rel_l2(yh, same) <= TOL_SAME
 
 
+# k % 256 == 0 takes the forward kernel with batched weight loads (two steps
+# of packed nibbles and four steps of absmax per load); the shapes above
+# with k % 256 != 0 take the per-step loads.
+BATCHED = [(1, 64, 256), (700, 300, 256), (513, 257, 512), (64, 130, 768), (640, 192, 1024)]
+
+
+@pytest.mark.parametrize("m,n,k", BATCHED)
+@pytest.mark.parametrize("dq_group", [0, 4, 8, 256])
+def test_fwd_batched_small_vs_oracle(m, n, k, dq_group):
+    w32 = oracle.gen_normal(31 + n + k, n * k, 0.02)
+    w = nf4.quantize_weight(torch.from_numpy(w32).to(DEV).view(n, k),
+                            double_quant=dq_group > 0, dq_group=dq_group or nf4.DQ_GROUP)
+    x, xh = _act(m, k, 9 + m)
+    y = gemm.linear_fwd(x, w)
+    torch.cuda.synchronize()
+    yh = y.float().cpu().numpy()
+    assert rel_l2(yh, oracle.matmul_tb(xh, _deq_host(w, f16=True))) <= TOL_REF
+    assert rel_l2(yh, oracle.matmul_tb(xh, _deq_host(w, f16=False))) <= TOL_SAME
+
+
+def _misaligned(t: torch.Tensor, by: int) -> torch.Tensor:
+    """A copy of t whose data pointer is `by` elements past an allocation."""
+    buf = torch.empty(t.numel() + by, dtype=t.dtype, device=t.device)
+    v = buf[by:by + t.numel()]
+    v.copy_(t)
+    return v
+
+
+@pytest.mark.parametrize("m,n,k", [(700, 300, 256), (513, 257, 1024), (1024, 256, 2048)])
+@pytest.mark.parametrize("dq", [False, True])
+def test_fwd_batched_equals_per_step(m, n, k, dq):
+    # The same weights through both forward kernels: absmax (or its codes)
+    # moved off the alignment the batched loads need selects the per-step
+    # kernel.  Same products, same reduction order: bit-identical outputs.
+    w = _weight(n, k, 41 + n + k, dq)
+    x, _ = _act(m, k, 13 + m)
+    y_batched = gemm.linear_fwd(x, w)
+    if dq:
+        w2 = nf4.Nf4Weight(packed=w.packed, absmax=None, shape=w.shape, absmax_q=_misaligned(w.absmax_q, 1),
+                           absmax_scale=w.absmax_scale, dq_group=w.dq_group)
+    else:
+        w2 = nf4.Nf4Weight(packed=w.packed, absmax=_misaligned(w.absmax, 1), shape=w.shape)
+    y_step = gemm.linear_fwd(x, w2)
+    torch.cuda.synchronize()
+    assert torch.equal(y_batched.view(torch.int16), y_step.view(torch.int16))
+
+
 @pytest.mark.parametrize("m,n,k", [(1, 64, 128), (64, 128, 64), (512, 128, 128),
                                    (700, 320, 300 - 300 % 64 + 64), (513, 256, 320)])
 @pytest.mark.parametrize("dq", [False, True])
