@@ -435,13 +435,13 @@ struct DgradProducer : PerStepLoads<kDQ, DgradProducer<kDQ>> {
   }
 };
 
-// Maps the workgroup index to (tile_m, tile_o).  Workgroups are dispatched
-// round-robin over the 8 XCDs; consecutive logical tiles (same activation
-// rows, neighbouring output columns) are given to the same XCD so that its
+// Maps tile index b to (tile_m, tile_o).  Workgroups are dispatched
+// round-robin over the 8 XCDs and the persistent grid is a multiple of 8, so
+// tile b runs on XCD b % 8; consecutive logical tiles (same activation rows,
+// neighbouring output columns) are given to the same XCD so that its
 // resident workgroups share the activation rows in that XCD's L2.
-__device__ __forceinline__ void map_tile(int tiles_m, int tiles_o, int &tm, int &to) {
+__device__ __forceinline__ void map_tile(int b, int tiles_m, int tiles_o, int &tm, int &to) {
   const int T = tiles_m * tiles_o;
-  const int b = blockIdx.x;
   const int x = b & 7, qq = b >> 3;
   const int base = T >> 3, rem = T & 7;
   const int L = x * base + (x < rem ? x : rem) + qq;
@@ -465,17 +465,19 @@ constexpr int kBufferFlags = 0x00020000;
 // s_waitcnt immediates (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] |
 // lgkmcnt[11:8] | vmcnt[5:4] << 14).
 constexpr int kWaitLgkm0 = 0xC07F;       // lgkmcnt(0), vmcnt and expcnt not waited
-constexpr int kWaitVm8Lgkm0 = 0x0078;    // vmcnt(8) lgkmcnt(0)
+// vmcnt(n) lgkmcnt(0), expcnt not waited.
+constexpr int wait_vm_lgkm0(int n) { return (n & 15) | 0x70 | ((n >> 4) << 14); }
 
 // Workgroup barrier without the memory-model fences of __syncthreads(): the
 // release fence would wait for every outstanding load (vmcnt(0)), including
 // the activation DMAs that are meant to stay in flight across it.  The waits
-// the barrier needs are issued explicitly before it (all but the 8 most
-// recent vector-memory operations, and every LDS operation); the empty asm
+// the barrier needs are issued explicitly before it (all but the kInFlight
+// most recent vector-memory operations, and every LDS operation); the empty asm
 // keeps the compiler from moving memory operations across it.
+template <int kInFlight>
 __device__ __forceinline__ void step_barrier() {
   __builtin_amdgcn_sched_barrier(0);
-  __builtin_amdgcn_s_waitcnt(kWaitVm8Lgkm0);
+  __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(kInFlight));
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
@@ -518,7 +520,10 @@ __device__ __forceinline__ void read_frag(const u32x4 *__restrict__ Acur,
 // In the dgrad plan some N/A slots also carry a P job: half of one word's
 // 16-bit transposed stores (dgrad_p_slot).  Each slot holds about the issue
 // time of one MFMA (32 cycles), and the 16 DMAs are spread over the step so
-// that the four waves of a CU never flood its texture-address unit.
+// that the four waves of a CU never flood its texture-address unit (all 16
+// in the second half of the step, with 16 exempt at the barrier, measured
+// 5-9 % slower).  The barrier exempts the 8 A jobs.
+constexpr int kDmaInFlight = 8;
 constexpr char kPlanFwd[57] =
     "RnRnLLNLLNLLNLLN"
     "RnRnWWWWWWWWWWWW"
@@ -532,7 +537,7 @@ constexpr char kPlanDgrad[57] =
 constexpr bool dgrad_p_slot(int n) {
   return n == 27 || n == 30 || n == 40 || n == 43 || n == 46 || n == 48 || n == 54 || n == 55;
 }
-// Number of jobs of kind c (of ('N' or 'n') when c is 'N') before slot n.
+// Number of jobs of kind c before slot n ('n' counts as N).
 constexpr int plan_index(const char *plan, int n, char c) {
   int k = 0;
   for (int i = 0; i < n; ++i) k += (plan[i] == c) || (c == 'N' && plan[i] == 'n');
@@ -548,12 +553,13 @@ constexpr int p_index(int n) {
 // tile in Acur (this wave's 128 rows) and the weight tile in Bcur.  Alongside
 // the MFMAs it reads the next sub-step's fragments, dequantizes step t+1's
 // packed weights (loaded by the producer in an earlier step) into Bnext,
-// issues the producer's loads for later steps and moves activation rows into LDS with
-// direct-to-LDS loads (1 KB = 8 whole 128-B rows per instruction): rows
-// 64-127 of step t+1 into Aoth (read last in step t-1) and rows 0-63 of step
-// t+2 into Acur after this wave's last reads of it.  Every DMA has at least
-// a sub-step to land before the barrier that precedes its reads, and the
-// barrier waits for all but the 8 most recent vector-memory operations.
+// issues the producer's loads for later steps and moves activation rows into
+// LDS with direct-to-LDS loads (1 KB = 8 whole 128-B rows per instruction):
+// rows 64-127 of step t+1 into Aoth (read last in step t-1) and rows 0-63 of
+// step t+2 into Acur after this wave's last reads of it.  Every DMA has at
+// least a sub-step to land before the barrier that precedes its reads, and
+// the barrier waits for all but the kDmaInFlight (8) most recent
+// vector-memory operations.
 // A wave issues in order, so other work only overlaps the matrix pipe when
 // it sits between MFMAs; sched_barrier fences keep the slot plan's order.
 //
@@ -666,7 +672,7 @@ __device__ __forceinline__ void gemm_step(const GemmArgs &g, Producer &prod,
     }
     __builtin_amdgcn_sched_barrier(0);
   });
-  step_barrier();
+  step_barrier<kDmaInFlight>();
   prod.template finish<kPhase>();
 }
 
@@ -696,8 +702,8 @@ __device__ __forceinline__ void gemm_main(const GemmArgs &g, Producer &prod,
   // Prologue: the producer's loads for steps 0 and 1, the activation tile of
   // step 0 and rows 0-63 of step 1 (DMA), then the weight tile of step 0
   // dequantized into B0.  The fences fix the order of issue, so that
-  // vmcnt(8) at the barrier means "all but step 1's 8 DMAs" to the compiler
-  // as to the hardware.
+  // vmcnt(kDmaInFlight) at the barrier means "all but step 1's 8 DMAs" to
+  // the compiler as to the hardware.
   prod.prologue_load(g, nsteps);
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -707,12 +713,12 @@ __device__ __forceinline__ void gemm_main(const GemmArgs &g, Producer &prod,
   __builtin_amdgcn_sched_barrier(0);
   const int step1 = (nsteps > 1) ? kStep * 2 : 0;
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+  for (int i = 0; i < kDmaInFlight; ++i)
     __builtin_amdgcn_raw_ptr_buffer_load_lds(arsrc, (lds_void_t *)(A1 + i * 64), 16,
                                              (int)aoff[i], step1, 0, 0);
   __builtin_amdgcn_sched_barrier(0);
   prod.prologue_store(B0);
-  step_barrier();
+  step_barrier<kDmaInFlight>();
 
   // Fragment registers; the first step's head multiplies zeros.
   u32x4 fa[2][4], fb[2][4];
@@ -752,26 +758,39 @@ __device__ __forceinline__ void gemm_main(const GemmArgs &g, Producer &prod,
   __builtin_amdgcn_s_waitcnt(0);
 }
 
-template <class Producer>
-__global__ void __launch_bounds__(kGemmThreads, 1) nf4_gemm_kernel(const GemmArgs g) {
-  int tm, to;
-  map_tile(g.tiles_m, g.tiles_o, tm, to);
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  const int jl = lane & 31;
-  const int grp = lane >> 5;
-  const int64_t m0 = (int64_t)tm * kTileM + wave * 128;
-  const int64_t o0 = (int64_t)to * kTileO;
-  const int64_t nsteps = g.R / kStep;
+// Up to kMaxGroups weights per launch.  Forward: the weights share the
+// activation x and each has its own output (q/k/v, gate/up); the output
+// tiles of all groups form one grid.  Input gradient: the groups are
+// reduction segments of one output, dx = sum_i dy_i . W_i.
+constexpr int kMaxGroups = 4;
+struct GemmGroup {
+  const uint16_t *a;   // input gradient: dy_i
+  int64_t lda;
+  uint16_t *out;       // forward: y_i
+  int64_t ldo;
+  const uint8_t *packed;
+  AbsmaxRef am;
+  int64_t wn;          // rows of W_i (its n)
+  int32_t tiles_o;     // forward: output tiles of this group
+};
+struct GroupedArgs {
+  GemmArgs base;       // shapes and the shared operand (x, or dx)
+  GemmGroup grp[kMaxGroups];
+  int32_t ngroups;
+  int32_t tiles_o;     // forward: output tiles over all groups
+};
 
-  // Direct-to-LDS activation loads: instruction i writes rows 8i..8i+7 of the
-  // wave's 128-row tile as 1 KB, lane p at LDS unit 64i + p, i.e. row
-  // 8i + p/8, physical unit p%8, which holds logical unit (p%8) ^ swz(row)
-  // (the swizzle of lds_unit).  aoff[i] is lane p's byte offset from the
-  // wave's first (clamped) row at k = 0; rows beyond M are clamped.  The
-  // loads go through a buffer resource based at that row, with the step's
-  // k offset in a scalar register, so the loop spends no vector ALU work on
-  // their addresses (check_gemm bounds every offset below 2^31).
+// Buffer resource and per-lane offsets of the wave's direct-to-LDS
+// activation loads: instruction i writes rows 8i..8i+7 of the wave's 128-row
+// tile as 1 KB, lane p at LDS unit 64i + p, i.e. row 8i + p/8, physical unit
+// p%8, which holds logical unit (p%8) ^ swz(row) (the swizzle of lds_unit).
+// aoff[i] is lane p's byte offset from the wave's first (clamped) row at
+// k = 0; rows beyond M are clamped.  The loads go through a buffer resource
+// based at that row, with the step's k offset in a scalar register, so the
+// loop spends no vector ALU work on their addresses (check_offsets bounds
+// every offset below 2^31).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t activation_setup(const GemmArgs &g, int64_t m0,
+                                                                   int lane, uint32_t (&aoff)[16]) {
   const int64_t mb = (m0 < g.M) ? m0 : g.M - 1;
   const char *abase = reinterpret_cast<const char *>(g.a + mb * g.lda);
   // Rows available to this wave from mb (at least 1, at most 128).
@@ -779,9 +798,6 @@ __global__ void __launch_bounds__(kGemmThreads, 1) nf4_gemm_kernel(const GemmArg
   const int32_t avail = (int32_t)(avail64 > 128 ? 128 : avail64);
   const uint32_t lda2 = (uint32_t)(g.lda * 2);
   const int32_t skip = (int32_t)(m0 - mb);  // > 0 only when the whole wave is past M
-  const __amdgpu_buffer_rsrc_t arsrc =
-      __builtin_amdgcn_make_buffer_rsrc((void *)abase, 0, 0x7fffffff, kBufferFlags);
-  uint32_t aoff[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int rr = 8 * i + (lane >> 3);
@@ -790,26 +806,25 @@ __global__ void __launch_bounds__(kGemmThreads, 1) nf4_gemm_kernel(const GemmArg
     const int u = (lane & 7) ^ swz(rr);
     aoff[i] = (uint32_t)rel * lda2 + 16u * (uint32_t)u;
   }
+  return __builtin_amdgcn_make_buffer_rsrc((void *)abase, 0, 0x7fffffff, kBufferFlags);
+}
 
-  Producer prod;
-  prod.init(g, o0, (uint32_t)(uintptr_t)(lds_void_t *)&g_lds_b[0][0]);
-
-  floatx16 acc[4][4];
+__device__ __forceinline__ void zero_acc(floatx16 (&acc)[4][4]) {
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[mt][nt][v] = 0.0f;
+}
 
-  gemm_main<Producer>(g, prod, acc, &g_lds_a[wave][0][0], &g_lds_a[wave][1][0], g_lds_b[0],
-                      g_lds_b[1], arsrc, aoff, nsteps, jl, grp);
-
-  // Epilogue: fp32 -> bf16 (RNE).  The MFMAs take the weight fragment as
-  // their first operand, so each accumulator tile is the transposed output
-  // block: lane l holds activation row m0 + 32mt + l%32 and output columns
-  // o0 + 32nt + 8j + 4g + i (i = 0..3) in registers 4j + i.  Four adjacent
-  // columns leave as one 8-byte store.
+// Epilogue: fp32 -> bf16 (RNE).  The MFMAs take the weight fragment as
+// their first operand, so each accumulator tile is the transposed output
+// block: lane l holds activation row m0 + 32mt + l%32 and output columns
+// o0 + 32nt + 8j + 4g + i (i = 0..3) in registers 4j + i.  Four adjacent
+// columns leave as one 8-byte store.
+__device__ __forceinline__ void store_tile(const GemmArgs &g, const floatx16 (&acc)[4][4],
+                                           int64_t m0, int64_t o0, int jl, int grp) {
   const bool vec_ok = ((reinterpret_cast<uintptr_t>(g.out) & 7) == 0) && ((g.ldo & 3) == 0);
   const int64_t cl = g.O - (o0 + 4 * grp);
   const int32_t clim = (int32_t)(cl < 0 ? 0 : (cl > (1 << 30) ? (1 << 30) : cl));
@@ -835,6 +850,161 @@ __global__ void __launch_bounds__(kGemmThreads, 1) nf4_gemm_kernel(const GemmArg
           }
         }
     }
+  }
+}
+
+// Epilogue through LDS, for outputs that take 16-byte stores (16-byte
+// aligned base, row stride a multiple of 8 elements).  Stores straight from
+// the accumulator layout write 16-byte pieces of 32 rows per instruction;
+// here each instruction writes 4 whole 256-byte rows of the wave's 128 x 128
+// tile, 8 times fewer L2 write requests for the same bytes.
+//  1. For each 32 x 32 accumulator tile, lanes l and l + 32 hold the two
+//     8-byte halves of 16-byte chunks (8 columns) of row l % 32.  One
+//     v_permlane32_swap per dword pairs them up: the lower lanes then hold
+//     chunk j, the upper lanes chunk j + 1, whole.
+//  2. The chunks go to the wave's own activation buffers (32 KB, idle after
+//     the last step), row r at 256 B * r, chunk c at physical chunk
+//     c ^ (r % 16): a 16-lane group of the ds_write_b128 covers 16 rows at
+//     one chunk, one of the ds_read_b128 16 chunks of one row, both spread
+//     over all banks.
+//  3. Lane p reads row 4i + p / 16, chunk p % 16 and stores 16 bytes.
+__device__ __forceinline__ void store_tile_lds(const GemmArgs &g, const floatx16 (&acc)[4][4],
+                                               u32x4 *lds, int64_t m0, int64_t o0, int lane) {
+  const int jl = lane & 31, grp = lane >> 5;
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) {
+    const int r = 32 * mt + jl;
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+      uint32_t lo[4], hi[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        lo[j] = pack_bf16x2(acc[mt][nt][4 * j], acc[mt][nt][4 * j + 1]);
+        hi[j] = pack_bf16x2(acc[mt][nt][4 * j + 2], acc[mt][nt][4 * j + 3]);
+      }
+#pragma unroll
+      for (int jp = 0; jp < 4; jp += 2) {
+        const auto a = __builtin_amdgcn_permlane32_swap(lo[jp], lo[jp + 1], false, false);
+        const auto b = __builtin_amdgcn_permlane32_swap(hi[jp], hi[jp + 1], false, false);
+        const uint32_t a0 = a[0], a1 = a[1], b0 = b[0], b1 = b[1];
+        const int c = 4 * nt + jp + grp;
+        lds[r * 16 + (c ^ (r & 15))] = (u32x4){a0, b0, a1, b1};
+      }
+    }
+  }
+  // The reads below take other lanes' writes: keep them after the writes.
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+  asm volatile("" ::: "memory");
+  const int c = lane & 15;
+  const int64_t col = o0 + 8 * c;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    const int r = 4 * i + (lane >> 4);
+    const u32x4 v = lds[r * 16 + (c ^ (r & 15))];
+    const int64_t m = m0 + r;
+    if (m < g.M) {
+      uint16_t *dst = g.out + m * g.ldo + col;
+      if (col + 8 <= g.O) {
+        *reinterpret_cast<u32x4 *>(dst) = v;
+      } else {
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (col + e < g.O) dst[e] = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
+      }
+    }
+  }
+}
+
+// The forward kernel's epilogue: through LDS when 16-byte stores fit.  (The
+// input-gradient kernel stores straight from the accumulators: its tiles
+// measured no faster through LDS.)
+__device__ __forceinline__ void epilogue(const GemmArgs &g, const floatx16 (&acc)[4][4], int wave,
+                                         int64_t m0, int64_t o0, int lane) {
+  if (((reinterpret_cast<uintptr_t>(g.out) & 15) == 0) && ((g.ldo & 7) == 0))
+    store_tile_lds(g, acc, &g_lds_a[wave][0][0], m0, o0, lane);
+  else
+    store_tile(g, acc, m0, o0, lane & 31, lane >> 5);
+}
+
+// Forward: y_i = x . W_i^T.  The grid covers tiles_m x (output tiles of all
+// groups); consecutive tiles share the activation rows (map_tile), also
+// across a group boundary.
+template <class Producer>
+__global__ void __launch_bounds__(kGemmThreads, 1) nf4_gemm_fwd_kernel(const GroupedArgs ga) {
+  const int T = ga.base.tiles_m * ga.tiles_o;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int jl = lane & 31;
+  const int grp = lane >> 5;
+#pragma unroll 1
+  for (int b = blockIdx.x; b < T; b += gridDim.x) {
+    GemmArgs g = ga.base;
+    int tm, to;
+    map_tile(b, g.tiles_m, ga.tiles_o, tm, to);
+    // The group of output tile `to` (uniform; at most kMaxGroups iterations).
+    int gi = 0;
+    while (gi + 1 < ga.ngroups && to >= ga.grp[gi].tiles_o) {
+      to -= ga.grp[gi].tiles_o;
+      ++gi;
+    }
+    g.out = ga.grp[gi].out;
+    g.ldo = ga.grp[gi].ldo;
+    g.packed = ga.grp[gi].packed;
+    g.am = ga.grp[gi].am;
+    g.wn = ga.grp[gi].wn;
+    g.O = ga.grp[gi].wn;
+    const int64_t m0 = (int64_t)tm * kTileM + wave * 128;
+    const int64_t o0 = (int64_t)to * kTileO;
+    uint32_t aoff[16];
+    const __amdgpu_buffer_rsrc_t arsrc = activation_setup(g, m0, lane, aoff);
+    Producer prod;
+    prod.init(g, o0, (uint32_t)(uintptr_t)(lds_void_t *)&g_lds_b[0][0]);
+    floatx16 acc[4][4];
+    zero_acc(acc);
+    gemm_main<Producer>(g, prod, acc, &g_lds_a[wave][0][0], &g_lds_a[wave][1][0], g_lds_b[0],
+                        g_lds_b[1], arsrc, aoff, g.R / kStep, jl, grp);
+    epilogue(g, acc, wave, m0, o0, lane);
+  }
+}
+
+// Input gradient: dx = sum_i dy_i . W_i, the groups run one after another
+// into the same accumulator.  Between two groups no barrier is needed: every
+// read of the shared weight tiles ended before the last step's barrier, and
+// the activation buffers are per wave.
+template <class Producer>
+__global__ void __launch_bounds__(kGemmThreads, 1) nf4_gemm_dgrad_kernel(const GroupedArgs ga) {
+  const int T = ga.base.tiles_m * ga.base.tiles_o;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int jl = lane & 31;
+  const int grp = lane >> 5;
+#pragma unroll 1
+  for (int b = blockIdx.x; b < T; b += gridDim.x) {
+    GemmArgs g = ga.base;
+    int tm, to;
+    map_tile(b, g.tiles_m, g.tiles_o, tm, to);
+    const int64_t m0 = (int64_t)tm * kTileM + wave * 128;
+    const int64_t o0 = (int64_t)to * kTileO;
+    floatx16 acc[4][4];
+    zero_acc(acc);
+#pragma unroll 1
+    for (int gi = 0; gi < ga.ngroups; ++gi) {
+      g.a = ga.grp[gi].a;
+      g.lda = ga.grp[gi].lda;
+      g.packed = ga.grp[gi].packed;
+      g.am = ga.grp[gi].am;
+      g.wn = ga.grp[gi].wn;
+      g.R = ga.grp[gi].wn;
+      uint32_t aoff[16];
+      const __amdgpu_buffer_rsrc_t arsrc = activation_setup(g, m0, lane, aoff);
+      Producer prod;
+      prod.init(g, o0, (uint32_t)(uintptr_t)(lds_void_t *)&g_lds_b[0][0]);
+      gemm_main<Producer>(g, prod, acc, &g_lds_a[wave][0][0], &g_lds_a[wave][1][0], g_lds_b[0],
+                          g_lds_b[1], arsrc, aoff, g.R / kStep, jl, grp);
+    }
+    store_tile(g, acc, m0, o0, jl, grp);
   }
 }
 
@@ -877,13 +1047,155 @@ static int32_t check_offsets(int64_t lda) {
   return NF4S_OK;
 }
 
+// A forward group can take the batched weight loads: whole 4-block absmax
+// groups per row (k % 256), aligned group loads, and 4-block groups inside
+// one double-quant scale.
+static bool fwd_batchable(const nf4s_tensor &w, int64_t k) {
+  if (k % 256 != 0) return false;
+  if (w.absmax_q != nullptr) return aligned(w.absmax_q, 4) && w.dq_group >= 4;
+  return aligned(w.absmax, 16);
+}
+
+static GemmGroup group_of(const nf4s_tensor &w, int64_t wn) {
+  GemmGroup q{};
+  q.packed = w.packed;
+  q.am = absmax_of(w);
+  q.wn = wn;
+  return q;
+}
+
+// Persistent grid: one workgroup per compute unit (a workgroup takes all of
+// a CU's LDS), each looping over tiles b, b + grid, ...  A tile's output
+// stores then drain while the same workgroup's next tile starts loading,
+// instead of every CU storing and then loading in lockstep at each round of
+// tiles.  The CU count is read once per device; a multiple of 8 keeps tile
+// b on XCD b % 8 (map_tile).
+static uint32_t persistent_grid(int64_t tiles) {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    cus[dev] = (n + 7) & ~7;
+  }
+  return (uint32_t)(tiles < cus[dev] ? tiles : cus[dev]);
+}
+
 template <class Producer>
-static int32_t launch_gemm(const GemmArgs &g, hipStream_t s, const char *name) {
-  const int64_t T = (int64_t)g.tiles_m * g.tiles_o;
+static int32_t launch_fwd(const GroupedArgs &ga, hipStream_t s) {
+  const int64_t T = (int64_t)ga.base.tiles_m * ga.tiles_o;
   if (T == 0) return NF4S_OK;
   if (T > 0x7fffffff) return fail(NF4S_ERR_UNSUPPORTED_SHAPE, "too many tiles");
-  hipLaunchKernelGGL(nf4_gemm_kernel<Producer>, dim3((uint32_t)T), dim3(kGemmThreads), 0, s, g);
-  return check_launch(name);
+  hipLaunchKernelGGL(nf4_gemm_fwd_kernel<Producer>, dim3(persistent_grid(T)), dim3(kGemmThreads),
+                     0, s, ga);
+  return check_launch("nf4_gemm_fwd");
+}
+
+template <class Producer>
+static int32_t launch_dgrad(const GroupedArgs &ga, hipStream_t s) {
+  const int64_t T = (int64_t)ga.base.tiles_m * ga.base.tiles_o;
+  if (T == 0) return NF4S_OK;
+  if (T > 0x7fffffff) return fail(NF4S_ERR_UNSUPPORTED_SHAPE, "too many tiles");
+  hipLaunchKernelGGL(nf4_gemm_dgrad_kernel<Producer>, dim3(persistent_grid(T)),
+                     dim3(kGemmThreads), 0, s, ga);
+  return check_launch("nf4_gemm_dgrad");
+}
+
+// Forward over `count` weights W_i [ns[i], k] sharing x [m, k]: y_i = x . W_i^T.
+// Weights of one kind (double-quantized or not, batched loads or not) share
+// a launch; a mixed set runs as one launch per kind.
+static int32_t gemm_fwd_groups(const uint16_t *x, const nf4s_tensor *ws, const int64_t *ns,
+                               uint16_t *const *ys, int32_t count, int64_t m, int64_t k,
+                               hipStream_t s) {
+  if (count <= 0 || count > kMaxGroups)
+    return fail(NF4S_ERR_INVALID_ARGUMENT, "count must be 1..%d, got %d", kMaxGroups, count);
+  if (ws == nullptr || ns == nullptr || ys == nullptr)
+    return fail(NF4S_ERR_INVALID_ARGUMENT, "weights, sizes or outputs are NULL");
+  int32_t rc = NF4S_OK;
+  for (int32_t i = 0; i < count && rc == NF4S_OK; ++i)
+    rc = check_gemm(x, &ws[i], m, ns[i], k, ys[i]);
+  if (rc == NF4S_OK) rc = check_offsets(k);
+  if (rc != NF4S_OK) return rc;
+  if (m == 0) return NF4S_OK;
+  // Kind of each weight: bit 0 double-quant, bit 1 batched loads.
+  int kind[kMaxGroups];
+  for (int32_t i = 0; i < count; ++i)
+    kind[i] = (ws[i].absmax_q != nullptr ? 1 : 0) | (fwd_batchable(ws[i], k) ? 2 : 0);
+  bool done[kMaxGroups] = {false, false, false, false};
+  for (int32_t i = 0; i < count; ++i) {
+    if (done[i]) continue;
+    GroupedArgs ga{};
+    GemmArgs &g = ga.base;
+    g.a = x;
+    g.lda = k;
+    g.M = m;
+    g.R = k;
+    g.wk = k;
+    g.tiles_m = (int32_t)((m + kTileM - 1) / kTileM);
+    int64_t tiles = 0;
+    for (int32_t j = i; j < count; ++j) {
+      if (done[j] || kind[j] != kind[i]) continue;
+      GemmGroup q = group_of(ws[j], ns[j]);
+      q.out = ys[j];
+      q.ldo = ns[j];
+      q.tiles_o = (int32_t)((ns[j] + kTileO - 1) / kTileO);
+      tiles += q.tiles_o;
+      ga.grp[ga.ngroups++] = q;
+      done[j] = true;
+    }
+    if (tiles > 0x7fffffff) return fail(NF4S_ERR_UNSUPPORTED_SHAPE, "too many tiles");
+    ga.tiles_o = (int32_t)tiles;
+    switch (kind[i]) {
+      case 3: rc = launch_fwd<FwdBatchProducer<true>>(ga, s); break;
+      case 2: rc = launch_fwd<FwdBatchProducer<false>>(ga, s); break;
+      case 1: rc = launch_fwd<FwdProducer<true>>(ga, s); break;
+      default: rc = launch_fwd<FwdProducer<false>>(ga, s); break;
+    }
+    if (rc != NF4S_OK) return rc;
+  }
+  return NF4S_OK;
+}
+
+// Input gradient dx [m, k] = sum_i dy_i [m, ns[i]] . W_i [ns[i], k].
+static int32_t gemm_dgrad_groups(const uint16_t *const *dys, const nf4s_tensor *ws,
+                                 const int64_t *ns, int32_t count, int64_t m, int64_t k,
+                                 uint16_t *dx, hipStream_t s) {
+  if (count <= 0 || count > kMaxGroups)
+    return fail(NF4S_ERR_INVALID_ARGUMENT, "count must be 1..%d, got %d", kMaxGroups, count);
+  if (dys == nullptr || ws == nullptr || ns == nullptr)
+    return fail(NF4S_ERR_INVALID_ARGUMENT, "gradients, weights or sizes are NULL");
+  const bool dq = ws[0].absmax_q != nullptr;
+  for (int32_t i = 0; i < count; ++i) {
+    int32_t rc = check_gemm(dys[i], &ws[i], m, ns[i], k, dx);
+    if (rc == NF4S_OK) rc = check_offsets(ns[i]);
+    if (rc != NF4S_OK) return rc;
+    if (ns[i] % 64 != 0)
+      return fail(NF4S_ERR_UNSUPPORTED_SHAPE, "dgrad needs n %% 64 == 0, got %lld",
+                  (long long)ns[i]);
+    if ((ws[i].absmax_q != nullptr) != dq)
+      return fail(NF4S_ERR_UNSUPPORTED_SHAPE,
+                  "summed dgrad needs all weights double-quantized or none");
+  }
+  if (m == 0) return NF4S_OK;
+  GroupedArgs ga{};
+  GemmArgs &g = ga.base;
+  g.out = dx;
+  g.ldo = k;
+  g.M = m;
+  g.O = k;
+  g.wk = k;
+  g.tiles_m = (int32_t)((m + kTileM - 1) / kTileM);
+  g.tiles_o = (int32_t)((k + kTileO - 1) / kTileO);
+  for (int32_t i = 0; i < count; ++i) {
+    GemmGroup q = group_of(ws[i], ns[i]);
+    q.a = dys[i];
+    q.lda = ns[i];
+    ga.grp[ga.ngroups++] = q;
+  }
+  return dq ? launch_dgrad<DgradProducer<true>>(ga, s) : launch_dgrad<DgradProducer<false>>(ga, s);
 }
 
 }  // namespace nf4s
@@ -894,62 +1206,27 @@ extern "C" {
 
 int32_t nf4s_gemm_fwd(const uint16_t *x, const nf4s_tensor *w, int64_t m, int64_t n, int64_t k,
                       uint16_t *y, void *stream) {
-  int32_t rc = check_gemm(x, w, m, n, k, y);
-  if (rc == NF4S_OK) rc = check_offsets(k);
-  if (rc != NF4S_OK) return rc;
-  if (m == 0) return NF4S_OK;
-  GemmArgs g{};
-  g.a = x;
-  g.lda = k;
-  g.out = y;
-  g.ldo = n;
-  g.M = m;
-  g.O = n;
-  g.R = k;
-  g.packed = w->packed;
-  g.am = absmax_of(*w);
-  g.wk = k;
-  g.wn = n;
-  g.tiles_m = (int32_t)((m + kTileM - 1) / kTileM);
-  g.tiles_o = (int32_t)((n + kTileO - 1) / kTileO);
-  // Batched weight loads need whole 4-block absmax groups per row (k % 256),
-  // aligned group loads, and 4-block groups inside one double-quant scale.
-  const bool dq = w->absmax_q != nullptr;
-  const bool batch = (k % 256 == 0) &&
-                     (dq ? (aligned(w->absmax_q, 4) && w->dq_group >= 4)
-                         : aligned(w->absmax, 16));
-  if (batch)
-    return dq ? launch_gemm<FwdBatchProducer<true>>(g, as_stream(stream), "nf4_gemm_fwd")
-              : launch_gemm<FwdBatchProducer<false>>(g, as_stream(stream), "nf4_gemm_fwd");
-  if (dq) return launch_gemm<FwdProducer<true>>(g, as_stream(stream), "nf4_gemm_fwd");
-  return launch_gemm<FwdProducer<false>>(g, as_stream(stream), "nf4_gemm_fwd");
+  if (w == nullptr) return fail(NF4S_ERR_INVALID_ARGUMENT, "weight descriptor is NULL");
+  uint16_t *ys[1] = {y};
+  return gemm_fwd_groups(x, w, &n, ys, 1, m, k, as_stream(stream));
 }
 
 int32_t nf4s_gemm_dgrad(const uint16_t *dy, const nf4s_tensor *w, int64_t m, int64_t n,
                         int64_t k, uint16_t *dx, void *stream) {
-  int32_t rc = check_gemm(dy, w, m, n, k, dx);
-  if (rc == NF4S_OK) rc = check_offsets(n);
-  if (rc != NF4S_OK) return rc;
-  if (n % 64 != 0)
-    return fail(NF4S_ERR_UNSUPPORTED_SHAPE, "dgrad needs n %% 64 == 0, got %lld", (long long)n);
-  if (m == 0) return NF4S_OK;
-  GemmArgs g{};
-  g.a = dy;
-  g.lda = n;
-  g.out = dx;
-  g.ldo = k;
-  g.M = m;
-  g.O = k;
-  g.R = n;
-  g.packed = w->packed;
-  g.am = absmax_of(*w);
-  g.wk = k;
-  g.wn = n;
-  g.tiles_m = (int32_t)((m + kTileM - 1) / kTileM);
-  g.tiles_o = (int32_t)((k + kTileO - 1) / kTileO);
-  if (w->absmax_q != nullptr)
-    return launch_gemm<DgradProducer<true>>(g, as_stream(stream), "nf4_gemm_dgrad");
-  return launch_gemm<DgradProducer<false>>(g, as_stream(stream), "nf4_gemm_dgrad");
+  if (w == nullptr) return fail(NF4S_ERR_INVALID_ARGUMENT, "weight descriptor is NULL");
+  const uint16_t *dys[1] = {dy};
+  return gemm_dgrad_groups(dys, w, &n, 1, m, k, dx, as_stream(stream));
+}
+
+int32_t nf4s_gemm_fwd_grouped(const uint16_t *x, const nf4s_tensor *ws, const int64_t *ns,
+                              uint16_t *const *ys, int32_t count, int64_t m, int64_t k,
+                              void *stream) {
+  return gemm_fwd_groups(x, ws, ns, ys, count, m, k, as_stream(stream));
+}
+
+int32_t nf4s_gemm_dgrad_sum(const uint16_t *const *dys, const nf4s_tensor *ws, const int64_t *ns,
+                            int32_t count, int64_t m, int64_t k, uint16_t *dx, void *stream) {
+  return gemm_dgrad_groups(dys, ws, ns, count, m, k, dx, as_stream(stream));
 }
 
 }  // extern "C"

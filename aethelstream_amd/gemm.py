@@ -6,6 +6,10 @@
                  doublepass/src/backward.rs:447-451).
 ``linear_dgrad`` dx = dy . W   replaces the dY.W loops of single_layer_backward
                  (doublepass/src/backward.rs:79-85,117-129,160-168,284-300).
+``linear_fwd_grouped``  y_i = x . W_i^T for weights sharing x, one launch
+                 (q/k/v at forward.rs:174-176, gate/up at forward.rs:251-252).
+``linear_dgrad_sum``    dx = sum_i dy_i . W_i, one launch and one rounding
+                 (d_h1 at backward.rs:284-300, d_h2 at backward.rs:117-129).
 
 x / dy are bf16 [M, K] / [M, N] device tensors, W an :class:`Nf4Weight` of
 shape [N, K]; accumulation is fp32 in MFMA, the output bf16.
@@ -13,7 +17,7 @@ shape [N, K]; accumulation is fp32 in MFMA, the output bf16.
 from __future__ import annotations
 
 import ctypes
-from typing import Optional
+from typing import List, Optional, Sequence
 
 import torch
 
@@ -55,6 +59,63 @@ def linear_dgrad(dy: torch.Tensor, w: Nf4Weight,
     desc = w.descriptor()
     _lib.check(_lib.load().nf4s_gemm_dgrad(dy.data_ptr(), ctypes.byref(desc), m, n, k,
                                            out.data_ptr(), _stream_ptr(dy)))
+    return out
+
+
+def _descs(ws: Sequence[Nf4Weight]):
+    arr = (_lib.Nf4sTensor * len(ws))()
+    for i, w in enumerate(ws):
+        arr[i] = w.descriptor()
+    return arr
+
+
+def linear_fwd_grouped(x: torch.Tensor, ws: Sequence[Nf4Weight],
+                       outs: Optional[Sequence[torch.Tensor]] = None) -> List[torch.Tensor]:
+    """[x . W_i^T for W_i in ws] (1..4 weights of one k) in one launch."""
+    if not 1 <= len(ws) <= 4:
+        raise ValueError("linear_fwd_grouped takes 1 to 4 weights")
+    k = int(ws[0].shape[1])
+    if any(int(w.shape[1]) != k for w in ws):
+        raise ValueError("grouped weights must share k")
+    _check_act(x, k, "x")
+    m = x.shape[0]
+    if outs is None:
+        outs = [torch.empty(m, int(w.shape[0]), dtype=torch.bfloat16, device=x.device)
+                for w in ws]
+    if len(outs) != len(ws):
+        raise ValueError("one output per weight")
+    for w, o in zip(ws, outs):
+        _check_act(o, int(w.shape[0]), "out")
+    ns = (ctypes.c_int64 * len(ws))(*[int(w.shape[0]) for w in ws])
+    ys = (ctypes.c_void_p * len(ws))(*[o.data_ptr() for o in outs])
+    descs = _descs(ws)
+    _lib.check(_lib.load().nf4s_gemm_fwd_grouped(x.data_ptr(), descs, ns, ys, len(ws), m, k,
+                                                 _stream_ptr(x)))
+    return list(outs)
+
+
+def linear_dgrad_sum(dys: Sequence[torch.Tensor], ws: Sequence[Nf4Weight],
+                     out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """sum_i dys[i] . W_i (1..4 weights of one k): one launch, fp32 accumulation
+    over all weights, one bf16 rounding."""
+    if not 1 <= len(ws) <= 4 or len(dys) != len(ws):
+        raise ValueError("linear_dgrad_sum takes 1 to 4 (dy, W) pairs")
+    k = int(ws[0].shape[1])
+    if any(int(w.shape[1]) != k for w in ws):
+        raise ValueError("summed weights must share k")
+    m = dys[0].shape[0]
+    for dy, w in zip(dys, ws):
+        _check_act(dy, int(w.shape[0]), "dy")
+        if dy.shape[0] != m:
+            raise ValueError("all dy must have the same number of rows")
+    if out is None:
+        out = torch.empty(m, k, dtype=torch.bfloat16, device=dys[0].device)
+    _check_act(out, k, "out")
+    ns = (ctypes.c_int64 * len(ws))(*[int(w.shape[0]) for w in ws])
+    dps = (ctypes.c_void_p * len(ws))(*[d.data_ptr() for d in dys])
+    descs = _descs(ws)
+    _lib.check(_lib.load().nf4s_gemm_dgrad_sum(dps, descs, ns, len(ws), m, k, out.data_ptr(),
+                                               _stream_ptr(out)))
     return out
 
 

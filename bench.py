@@ -175,13 +175,15 @@ def bench_gemm(torch, nf4, gemm, args):
     acts = [x, x, xd]
 
     def cfg3():
-        for a, w, y in zip(acts, ws, ys):
-            gemm.linear_fwd(a, w, y)
+        # gate and up share x: one grouped launch (forward.rs:251-252).
+        gemm.linear_fwd_grouped(x, ws[:2], ys[:2])
+        gemm.linear_fwd(xd, ws[2], ys[2])
     steps = max(3, args.steps // 5)
     ms3 = timed(torch, cfg3, steps, 2)
     fl3 = sum(2.0 * 4096 * w.shape[0] * w.shape[1] for w in ws)
     tf3 = fl3 / (ms3 * 1e-3) / 1e12
     res["config3_7b_mlp_fwd"] = {"tflops": round(tf3, 1), "ms": round(ms3, 4), "flop": fl3,
+                                 "launches": "[gate,up] grouped, down",
                                  "frac_of_bf16_peak": round(tf3 / BF16_PEAK_TFLOPS, 4)}
     del ws, x, xd, ys, acts
     torch.cuda.empty_cache()
@@ -198,13 +200,21 @@ def bench_gemm(torch, nf4, gemm, args):
     dys = [torch.randn(M, w.shape[0], device="cuda", generator=g).to(torch.bfloat16) for w in ws]
     dxs = [torch.empty(M, w.shape[1], dtype=torch.bfloat16, device="cuda") for w in ws]
 
+    # The layer's GEMMs as single_layer_forward / single_layer_backward
+    # issue them: q/k/v and gate/up share their input (forward.rs:174-176,
+    # 251-252); the input gradients of q/k/v and of gate/up are sums
+    # (backward.rs:284-300, 117-129).
     def fwd_pass():
-        for a, w, y in zip(ins, ws, ys):
-            gemm.linear_fwd(a, w, y)
+        gemm.linear_fwd_grouped(h, ws[0:3], ys[0:3])        # q, k, v
+        gemm.linear_fwd(h, ws[3], ys[3])                    # o
+        gemm.linear_fwd_grouped(h, ws[4:6], ys[4:6])        # gate, up
+        gemm.linear_fwd(hid, ws[6], ys[6])                  # down
 
     def dgrad_pass():
-        for dy, w, dx in zip(dys, ws, dxs):
-            gemm.linear_dgrad(dy, w, dx)
+        gemm.linear_dgrad_sum(dys[0:3], ws[0:3], dxs[0])    # d_h1
+        gemm.linear_dgrad(dys[3], ws[3], dxs[3])            # d_attn_out
+        gemm.linear_dgrad_sum(dys[4:6], ws[4:6], dxs[4])    # d_h2
+        gemm.linear_dgrad(dys[6], ws[6], dxs[6])            # d_hidden
 
     def layer_step():
         fwd_pass()      # forward
@@ -227,6 +237,8 @@ def bench_gemm(torch, nf4, gemm, args):
     res["config4_70b_layer"] = {
         "tflops": round(tf_l, 1), "ms_per_layer_step": round(ms_l, 3),
         "flop_per_pass": fl_pass, "passes": 3,
+        "launches": "fwd: [q,k,v] grouped, o, [gate,up] grouped, down; dgrad: dq.Wq+dk.Wk+dv.Wv "
+                    "summed, o, d_gate.Wg+d_up.Wu summed, down",
         "frac_of_bf16_peak": round(tf_l / BF16_PEAK_TFLOPS, 4),
         "fwd_pass_tflops": round(fl_pass / (ms_f * 1e-3) / 1e12, 1),
         "dgrad_pass_tflops": round(fl_pass / (ms_d * 1e-3) / 1e12, 1),
@@ -263,8 +275,10 @@ def bench_stream(torch, nf4, gemm, nlayers, M=4096):
     comp = torch.cuda.current_stream()
 
     def compute(l, views):
-        for a, w, y in zip(ins, views, outs):
-            gemm.linear_fwd(a, w, y)
+        gemm.linear_fwd_grouped(x, views[0:3], outs[0:3])
+        gemm.linear_fwd(x, views[3], outs[3])
+        gemm.linear_fwd_grouped(x, views[4:6], outs[4:6])
+        gemm.linear_fwd(hid, views[6], outs[6])
 
     def wall(fn):
         torch.cuda.synchronize()

@@ -137,6 +137,33 @@ int32_t nf4s_gemm_fwd(const uint16_t *x, const nf4s_tensor *w, int64_t m,
 int32_t nf4s_gemm_dgrad(const uint16_t *dy, const nf4s_tensor *w, int64_t m,
                         int64_t n, int64_t k, uint16_t *dx, void *stream);
 
+/*
+ * Grouped forward: y_i[m, ns[i]] = x[m,k] . W_i^T for `count` (1..4) NF4
+ * weights W_i [ns[i], k] that share the activation x, in one launch whose
+ * output tiles span all the weights.  Replaces the matmul_tb calls that share
+ * their input in single_layer_forward: q/k/v (doublepass/src/forward.rs:174-176)
+ * and gate/up (forward.rs:251-252).  Same requirements as nf4s_gemm_fwd for
+ * each weight; weights of different kinds (double-quantized or not) run as
+ * one launch per kind.
+ */
+int32_t nf4s_gemm_fwd_grouped(const uint16_t *x, const nf4s_tensor *ws,
+                              const int64_t *ns, uint16_t *const *ys,
+                              int32_t count, int64_t m, int64_t k,
+                              void *stream);
+
+/*
+ * Summed input gradient: dx[m,k] = sum_i dy_i[m, ns[i]] . W_i for `count`
+ * (1..4) NF4 weights W_i [ns[i], k], one launch, one fp32 accumulator per
+ * output element, one bf16 rounding.  Replaces the accumulating dY.W loops
+ * of single_layer_backward: d_h1 = dq.Wq + dk.Wk + dv.Wv
+ * (doublepass/src/backward.rs:284-300) and d_h2 = d_gate.Wg + d_up.Wu
+ * (backward.rs:117-129).  Each ns[i] % 64 == 0; the weights are all
+ * double-quantized or all not.
+ */
+int32_t nf4s_gemm_dgrad_sum(const uint16_t *const *dys, const nf4s_tensor *ws,
+                            const int64_t *ns, int32_t count, int64_t m,
+                            int64_t k, uint16_t *dx, void *stream);
+
 /* ---------------------------------------------------------------------------
  * Streamed layer stack (one GPU).  Layers wait in pinned host memory and are
  * copied into a two-slot device double buffer on a dedicated copy stream.

@@ -201,3 +201,69 @@ def test_gemm_argument_errors():
     dy = torch.zeros(4, 96, dtype=torch.bfloat16, device=DEV)
     with pytest.raises(Exception, match="n % 64"):
         gemm.linear_dgrad(dy, w)
+
+
+# Grouped launches: forward over weights that share x (q/k/v, gate/up) and
+# the summed input gradient (d_h1 = dq.Wq + dk.Wk + dv.Wv, d_h2 = d_gate.Wg +
+# d_up.Wu).
+
+@pytest.mark.parametrize("m,k,ns,dqs", [
+    (700, 256, [300, 64, 130], [True, True, True]),        # batched loads, ragged
+    (513, 320, [257, 128], [False, False]),                # per-step loads
+    (640, 512, [384, 128, 128, 200], [True, False, True, False]),  # mixed kinds
+])
+def test_fwd_grouped_equals_separate(m, k, ns, dqs):
+    ws = [_weight(n, k, 51 + i * 7 + n, dq) for i, (n, dq) in enumerate(zip(ns, dqs))]
+    x, _ = _act(m, k, 17 + m)
+    ys = gemm.linear_fwd_grouped(x, ws)
+    sep = [gemm.linear_fwd(x, w) for w in ws]
+    torch.cuda.synchronize()
+    for y, s in zip(ys, sep):
+        assert torch.equal(y.view(torch.int16), s.view(torch.int16))
+
+
+@pytest.mark.parametrize("m,k,ns", [(700, 192, [128, 64, 64]), (513, 256, [320, 128]),
+                                    (64, 128, [64]), (1024, 512, [256, 64, 64, 128])])
+@pytest.mark.parametrize("dq", [False, True])
+def test_dgrad_sum_small_vs_oracle(m, k, ns, dq):
+    ws = [_weight(n, k, 61 + i * 5 + n, dq) for i, n in enumerate(ns)]
+    acts = [_act(m, n, 23 + i + m) for i, n in enumerate(ns)]
+    dx = gemm.linear_dgrad_sum([a for a, _ in acts], ws)
+    torch.cuda.synchronize()
+    dxh = dx.float().cpu().numpy()
+    ref = sum(oracle.dgrad(ah, _deq_host(w, f16=True)) for (_, ah), w in zip(acts, ws))
+    assert rel_l2(dxh, ref) <= TOL_REF
+    same = sum(oracle.dgrad(ah, _deq_host(w, f16=False)).astype(np.float64)
+               for (_, ah), w in zip(acts, ws))
+    assert rel_l2(dxh, same) <= TOL_SAME
+
+
+@pytest.mark.parametrize("name,ns,k", [("d_h1 = dq.Wq + dk.Wk + dv.Wv", [8192, 1024, 1024], 8192),
+                                       ("d_h2 = d_gate.Wg + d_up.Wu", [28672, 28672], 8192)])
+def test_dgrad_sum_70b_shapes(name, ns, k):
+    # BASELINE config 4 input gradients as the reference accumulates them.
+    m = 8192
+    g = torch.Generator(device=DEV).manual_seed(8)
+    ws = [nf4.quantize_weight(torch.randn(n, k, device=DEV, generator=g) * 0.02, double_quant=True)
+          for n in ns]
+    dys = [torch.randn(m, n, device=DEV, generator=g).to(torch.bfloat16) for n in ns]
+    dx = gemm.linear_dgrad_sum(dys, ws)
+    ref = torch.zeros(m, k, device=DEV)
+    for dy, w in zip(dys, ws):
+        ref += dy.float() @ nf4.dequant(w).float()
+    torch.cuda.synchronize()
+    err = ((dx.float() - ref).norm() / ref.norm()).item()
+    assert err <= TOL_SAME, err
+    del ws, dys, dx, ref
+
+
+def test_grouped_argument_errors():
+    w = _weight(128, 128, 2)
+    wq = _weight(128, 128, 3, dq=True)
+    x = torch.zeros(4, 128, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(ValueError):
+        gemm.linear_fwd_grouped(x, [])
+    with pytest.raises(ValueError):
+        gemm.linear_fwd_grouped(x, [w] * 5)
+    with pytest.raises(Exception, match="double-quantized"):
+        gemm.linear_dgrad_sum([x, x], [w, wq])
