@@ -18,9 +18,17 @@ Under "stream", config 5: 80 70B layers in pinned host memory streamed
 through a two-slot device buffer (H2D on a copy stream) while the previous
 layer's forward GEMMs run, 4096 tokens: layers/s, H2D GB/s, overlap.
 
+Also under "gemm": "bf16_gemm_reference", a plain bf16 GEMM (torch.matmul,
+hipBLASLt) of the 70B gate shape on the same box, and what an unfused path
+(dequantize the layer to bf16, then that GEMM rate) would reach on config 4.
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
                        [--workload all|dequant|gemm|stream] [--stream-layers L]
                        [--copy-calibration]
+                       [--gemm-shape NAME [--gemm-mode fwd|dgrad]]
+  --gemm-shape times one fused GEMM (70b_q, 70b_k, 70b_gate, 70b_down, 7b_gate,
+  7b_down) `steps` times after `warmup` and prints only its line (profiling);
+  --gemm-mode bf16-reference times torch.matmul in bf16 on that shape instead.
 """
 from __future__ import annotations
 
@@ -40,6 +48,10 @@ LAYER_7B = [("q", 4096, 4096), ("k", 4096, 4096), ("v", 4096, 4096), ("o", 4096,
 GEMM_7B = [("gate", 11008, 4096), ("up", 11008, 4096), ("down", 4096, 11008)]
 LAYER_70B = [("q", 8192, 8192), ("k", 1024, 8192), ("v", 1024, 8192), ("o", 8192, 8192),
              ("gate", 28672, 8192), ("up", 28672, 8192), ("down", 8192, 28672)]
+# name -> (tokens M, W rows N, W columns K)
+GEMM_SHAPES = {"70b_q": (8192, 8192, 8192), "70b_k": (8192, 1024, 8192),
+               "70b_gate": (8192, 28672, 8192), "70b_down": (8192, 8192, 28672),
+               "7b_gate": (4096, 11008, 4096), "7b_down": (4096, 4096, 11008)}
 
 
 def algorithmic_bytes_dq(shapes, bs=64, group=256) -> int:
@@ -64,6 +76,10 @@ def parse():
                     help="config 5: number of 70B layers held in pinned host memory")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device-to-device copy (PMC byte calibration)")
+    ap.add_argument("--gemm-shape", choices=sorted(GEMM_SHAPES), default=None,
+                    help="only time one fused GEMM shape (for profiling)")
+    ap.add_argument("--gemm-mode", choices=["fwd", "dgrad", "bf16-reference"], default="fwd",
+                    help="bf16-reference: torch.matmul (hipBLASLt) of the same shape in bf16")
     return ap.parse_args()
 
 
@@ -323,6 +339,52 @@ def bench_stream(torch, nf4, gemm, nlayers, M=4096):
     }
 
 
+def bench_one_gemm(torch, nf4, gemm, args):
+    """One fused GEMM shape, args.steps timed launches (HIP events)."""
+    m, n, k = GEMM_SHAPES[args.gemm_shape]
+    g = torch.Generator(device="cuda").manual_seed(7)
+    w = nf4.quantize_weight(torch.randn(n, k, device="cuda", generator=g) * 0.02, double_quant=True)
+    if args.gemm_mode == "fwd":
+        a = torch.randn(m, k, device="cuda", generator=g).to(torch.bfloat16)
+        o = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
+        fn = lambda: gemm.linear_fwd(a, w, o)
+    elif args.gemm_mode == "bf16-reference":
+        a = torch.randn(m, k, device="cuda", generator=g).to(torch.bfloat16)
+        b = torch.randn(n, k, device="cuda", generator=g).to(torch.bfloat16)
+        o = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
+        fn = lambda: torch.matmul(a, b.t(), out=o)
+    else:
+        a = torch.randn(m, n, device="cuda", generator=g).to(torch.bfloat16)
+        o = torch.empty(m, k, dtype=torch.bfloat16, device="cuda")
+        fn = lambda: gemm.linear_dgrad(a, w, o)
+    ms = timed(torch, fn, args.steps, args.warmup)
+    tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+    print(json.dumps({"gemm_shape": args.gemm_shape, "mode": args.gemm_mode, "m": m, "n": n,
+                      "k": k, "ms": round(ms, 4), "tflops": round(tf, 1)}), flush=True)
+
+
+def bf16_gemm_reference(torch, dequant_gbs, layer_ms):
+    """A plain bf16 GEMM (torch.matmul -> hipBLASLt) of the 70B gate shape, and
+    the config-4 rate of an unfused path: dequantize each pass's weights to
+    bf16 (at the measured dequant rate), then GEMMs at that plain rate."""
+    m, n, k = GEMM_SHAPES["70b_gate"]
+    g = torch.Generator(device="cuda").manual_seed(9)
+    a = torch.randn(m, k, device="cuda", generator=g).to(torch.bfloat16)
+    b = torch.randn(n, k, device="cuda", generator=g).to(torch.bfloat16)
+    o = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
+    ms = timed(torch, lambda: torch.matmul(a, b.t(), out=o), 5, 2)
+    tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+    res = {"op": "torch.matmul bf16 (hipBLASLt), M=8192 N=28672 K=8192", "tflops": round(tf, 1),
+           "frac_of_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4)}
+    if dequant_gbs and layer_ms:
+        fl_pass = sum(2.0 * 8192 * r * c for _, r, c in LAYER_70B)
+        deq_ms = algorithmic_bytes_dq(LAYER_70B) / (dequant_gbs * 1e9) * 1e3
+        unfused_ms = 3 * (deq_ms + fl_pass / (tf * 1e12) * 1e3)
+        res["unfused_config4_tflops"] = round(3 * fl_pass / (unfused_ms * 1e-3) / 1e12, 1)
+        res["fused_over_unfused"] = round(unfused_ms / layer_ms, 3)
+    return res
+
+
 def copy_calibration(torch):
     """A plain device copy of exactly 1 GiB read + 1 GiB written (the known
     byte count that rocprofv3's FETCH_SIZE / WRITE_SIZE are scaled against)."""
@@ -350,6 +412,9 @@ def main():
         copy_calibration(torch)
         return
     from aethelstream_amd import gemm, nf4
+    if args.gemm_shape:
+        bench_one_gemm(torch, nf4, gemm, args)
+        return
 
     line = {
         "metric": "NF4 dequant HBM GB/s (% peak); NF4-fused GEMM TFLOP/s at 7B/70B layer shapes",
@@ -378,6 +443,9 @@ def main():
     if args.workload in ("all", "gemm"):
         line["gemm"] = bench_gemm(torch, nf4, gemm, args)
         line["gemm"]["peak_tflops"] = BF16_PEAK_TFLOPS
+        log("plain bf16 GEMM reference")
+        line["gemm"]["bf16_gemm_reference"] = bf16_gemm_reference(
+            torch, line.get("value"), line["gemm"]["config4_70b_layer"]["ms_per_layer_step"])
     if args.workload in ("all", "stream"):
         log(f"config 5: {args.stream_layers} streamed 70B layers")
         try:
