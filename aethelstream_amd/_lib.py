@@ -71,6 +71,9 @@ SIGNATURES = {
     "nf4s_last_error_message": (ctypes.c_char_p, []),
     "nf4s_quantize": (_I32, [_P, _I64, _I32, _P, _P, _P]),
     "nf4s_dq_encode": (_I32, [_P, _I64, _I32, _P, _P, _P]),
+    "nf4s_quantize_bf16": (_I32, [_P, _I64, _I32, _P, _P, _P]),
+    "nf4s_quantize_dq": (_I32, [_P, _I64, _I32, _I32, _P, _P, _P, _P]),
+    "nf4s_quantize_dq_bf16": (_I32, [_P, _I64, _I32, _I32, _P, _P, _P, _P]),
     "nf4s_dequant_f16": (_I32, [_TP, _I64, _P, _P]),
     "nf4s_dequant_bf16": (_I32, [_TP, _I64, _P, _P]),
     "nf4s_dequant_batch_bf16": (_I32, [_TP, ctypes.POINTER(_I64), ctypes.POINTER(_P), _I32, _P]),

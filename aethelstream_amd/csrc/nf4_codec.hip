@@ -50,8 +50,41 @@ __device__ __forceinline__ uint32_t nf4_code(float n) {
   return dr < dl ? (uint32_t)(j + 1) : (uint32_t)j;
 }
 
-// block_size == 64: one wave per block, one lane per element.
-__global__ void __launch_bounds__(256) quantize64_kernel(const float *__restrict__ x, int64_t n,
+// Element e of the input: fp32, or bf16 widened exactly (the bf16 weights a
+// bf16 update leaves, doublepass/src/precision.rs:187-202).
+template <typename T>
+__device__ __forceinline__ float load_elem(const T *x, int64_t e);
+template <>
+__device__ __forceinline__ float load_elem<float>(const float *x, int64_t e) {
+  return x[e];
+}
+template <>
+__device__ __forceinline__ float load_elem<uint16_t>(const uint16_t *x, int64_t e) {
+  return __builtin_bit_cast(float, (uint32_t)x[e] << 16);
+}
+
+// One 64-element block by one wave, one lane per element: returns the block's
+// unclamped absmax (in every lane) and writes its packed codes.
+template <typename T>
+__device__ __forceinline__ float quantize_block64(const T *__restrict__ x, int64_t n, int64_t b,
+                                                  int lane, uint8_t *__restrict__ packed) {
+  const int64_t e = b * 64 + lane;
+  const float v = (e < n) ? load_elem<T>(x, e) : 0.0f;  // zero padding, quantizer.py:30-32
+  float m = fabsf(v);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) m = max_nan(m, __shfl_xor(m, off, 64));
+  const float safe = (m < 1e-8f) ? 1e-8f : m;          // clamp(min=1e-8), :36
+  const float nv = v / safe;                           // correctly rounded, :38
+  uint32_t c = nf4_code(nv);
+  uint32_t c1 = __shfl_xor(c, 1, 64);
+  if (e + 1 >= n) c1 = 0;                              // odd-count pad nibble, :44-45
+  if ((lane & 1) == 0 && e < n) packed[e >> 1] = (uint8_t)((c << 4) | c1);  // :46
+  return m;                                            // unclamped, :48-53
+}
+
+// block_size == 64: one wave per block.
+template <typename T>
+__global__ void __launch_bounds__(256) quantize64_kernel(const T *__restrict__ x, int64_t n,
                                                          uint8_t *__restrict__ packed,
                                                          float *__restrict__ absmax,
                                                          int64_t nblocks) {
@@ -59,18 +92,8 @@ __global__ void __launch_bounds__(256) quantize64_kernel(const float *__restrict
   const int64_t wave0 = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   const int64_t nwaves = (int64_t)gridDim.x * (blockDim.x >> 6);
   for (int64_t b = wave0; b < nblocks; b += nwaves) {
-    const int64_t e = b * 64 + lane;
-    const float v = (e < n) ? x[e] : 0.0f;  // zero padding, quantizer.py:30-32
-    float m = fabsf(v);
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) m = max_nan(m, __shfl_xor(m, off, 64));
-    if (lane == 0) absmax[b] = m;                        // unclamped, :48-53
-    const float safe = (m < 1e-8f) ? 1e-8f : m;          // clamp(min=1e-8), :36
-    const float nv = v / safe;                           // correctly rounded, :38
-    uint32_t c = nf4_code(nv);
-    uint32_t c1 = __shfl_xor(c, 1, 64);
-    if (e + 1 >= n) c1 = 0;                              // odd-count pad nibble, :44-45
-    if ((lane & 1) == 0 && e < n) packed[e >> 1] = (uint8_t)((c << 4) | c1);  // :46
+    const float m = quantize_block64<T>(x, n, b, lane, packed);
+    if (lane == 0) absmax[b] = m;
   }
 }
 
@@ -111,6 +134,17 @@ __global__ void codes_generic_kernel(const float *__restrict__ x, int64_t n, int
 // Double-quant encode (conventions of galore/src/quantize.rs:4-13)
 // ---------------------------------------------------------------------------
 
+// Scale of a double-quant group from its largest absmax (1.0 for an all-zero
+// group, galore/src/quantize.rs:8-12), and the code of one absmax: round
+// half to even, clamped to 0..127 (NaN -> 0).
+__device__ __forceinline__ float dq_scale(float mx) { return (mx <= 0.0f) ? 1.0f : mx / 127.0f; }
+__device__ __forceinline__ uint8_t dq_code(float a, float sc) {
+  float r = rintf(a / sc);  // round half to even
+  if (!(r >= 0.0f)) r = 0.0f;
+  if (r > 127.0f) r = 127.0f;
+  return (uint8_t)r;
+}
+
 __global__ void __launch_bounds__(256) dq_encode_kernel(const float *__restrict__ absmax,
                                                         int64_t nblocks, int32_t group,
                                                         uint8_t *__restrict__ q,
@@ -133,14 +167,52 @@ __global__ void __launch_bounds__(256) dq_encode_kernel(const float *__restrict_
   __syncthreads();
   float mx = red[0];
   for (int w = 1; w < (int)(blockDim.x >> 6); ++w) mx = (red[w] > mx) ? red[w] : mx;
-  const float sc = (mx <= 0.0f) ? 1.0f : mx / 127.0f;
+  const float sc = dq_scale(mx);
   if (threadIdx.x == 0) scale[g] = sc;
-  for (int64_t i = s + threadIdx.x; i < e; i += blockDim.x) {
-    float r = rintf(absmax[i] / sc);  // round half to even
-    if (!(r >= 0.0f)) r = 0.0f;
-    if (r > 127.0f) r = 127.0f;
-    q[i] = (uint8_t)r;
+  for (int64_t i = s + threadIdx.x; i < e; i += blockDim.x) q[i] = dq_code(absmax[i], sc);
+}
+
+// Quantize + double-quant in one pass, for weights re-quantized on the device
+// after an update (FlowCast::on_weights_updated, flowcast/src/lib.rs:501-521,
+// after apply_galore_bf16_update, doublepass/src/precision.rs:187-202): one
+// workgroup per group of `group` 64-element blocks.
+// The block absmax stay in LDS (never written as fp32), so the call needs no
+// scratch memory; codes come from the fp32 absmax exactly as quantize64_kernel
+// computes them, and q / scale exactly as dq_encode_kernel does.
+template <typename T>
+__global__ void __launch_bounds__(256) quantize_dq_kernel(const T *__restrict__ x, int64_t n,
+                                                          int32_t group,
+                                                          uint8_t *__restrict__ packed,
+                                                          uint8_t *__restrict__ q,
+                                                          float *__restrict__ scale,
+                                                          int64_t nblocks) {
+  extern __shared__ float am_lds[];  // `group` block absmax
+  __shared__ float red[4];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t b0 = (int64_t)blockIdx.x * group;
+  const int64_t nb = (b0 + group < nblocks) ? group : nblocks - b0;
+  for (int64_t i = wave; i < nb; i += 4) {
+    const float m = quantize_block64<T>(x, n, b0 + i, lane, packed);
+    if (lane == 0) am_lds[i] = m;
   }
+  __syncthreads();
+  float m = 0.0f;
+  for (int64_t i = threadIdx.x; i < nb; i += blockDim.x) {
+    const float a = am_lds[i];
+    m = (a > m) ? a : m;  // NaN never wins, as in dq_encode_kernel
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float o = __shfl_xor(m, off, 64);
+    m = (o > m) ? o : m;
+  }
+  if (lane == 0) red[wave] = m;
+  __syncthreads();
+  float mx = red[0];
+  for (int w = 1; w < 4; ++w) mx = (red[w] > mx) ? red[w] : mx;
+  const float sc = dq_scale(mx);
+  if (threadIdx.x == 0) scale[blockIdx.x] = sc;
+  for (int64_t i = threadIdx.x; i < nb; i += blockDim.x) q[b0 + i] = dq_code(am_lds[i], sc);
 }
 
 // ---------------------------------------------------------------------------
@@ -148,6 +220,7 @@ __global__ void __launch_bounds__(256) dq_encode_kernel(const float *__restrict_
 // ---------------------------------------------------------------------------
 
 constexpr int kMaxBatch = 16;
+constexpr int32_t kMaxDqGroup = 8192;  // quantize_dq_kernel keeps a group's absmax in LDS
 constexpr int kDqThreads = 256;                   // 4 waves
 constexpr int kDqRounds = 2;                      // rounds of 64 chunks per wave
 constexpr int64_t kTileChunks = 4LL * 64 * kDqRounds;
@@ -316,6 +389,28 @@ static int32_t dequant_batch(const nf4s_tensor *ts, const int64_t *ns, uint16_t 
   return NF4S_OK;
 }
 
+template <typename T>
+static int32_t quantize_dq(const T *x, int64_t n, int32_t block_size, int32_t group,
+                           uint8_t *packed, uint8_t *q, float *scale, void *stream) {
+  if (n < 0) return fail(NF4S_ERR_INVALID_ARGUMENT, "negative element count");
+  if (block_size != 64)
+    return fail(NF4S_ERR_UNSUPPORTED_SHAPE, "quantize + double-quant needs block_size 64, got %d",
+                block_size);
+  if (group <= 0 || (group & (group - 1)) != 0 || group > kMaxDqGroup)
+    return fail(NF4S_ERR_INVALID_ARGUMENT, "group must be a power of two <= %d, got %d",
+                kMaxDqGroup, group);
+  if (n == 0) return NF4S_OK;
+  if (x == nullptr || packed == nullptr || q == nullptr || scale == nullptr)
+    return fail(NF4S_ERR_INVALID_ARGUMENT, "NULL buffer");
+  const int64_t nb = (n + 63) / 64;
+  const int64_t ng = (nb + group - 1) / group;
+  if (ng > 0x7fffffff) return fail(NF4S_ERR_UNSUPPORTED_SHAPE, "too many groups");
+  hipLaunchKernelGGL(quantize_dq_kernel<T>, dim3((uint32_t)ng), dim3(256),
+                     (size_t)group * sizeof(float), as_stream(stream), x, n, group, packed, q,
+                     scale, nb);
+  return check_launch("quantize_dq_kernel");
+}
+
 }  // namespace nf4s
 
 using namespace nf4s;
@@ -333,8 +428,8 @@ int32_t nf4s_quantize(const float *x, int64_t n, int32_t block_size, uint8_t *pa
   hipStream_t s = as_stream(stream);
   if (block_size == 64) {
     const int64_t wg = (nb + 3) / 4;
-    hipLaunchKernelGGL(quantize64_kernel, dim3(grid_for(wg, 1)), dim3(256), 0, s, x, n, packed,
-                       absmax, nb);
+    hipLaunchKernelGGL(quantize64_kernel<float>, dim3(grid_for(wg, 1)), dim3(256), 0, s, x, n,
+                       packed, absmax, nb);
     return check_launch("quantize64_kernel");
   }
   hipLaunchKernelGGL(absmax_generic_kernel, dim3(grid_for(nb, 256)), dim3(256), 0, s, x, n,
@@ -345,6 +440,32 @@ int32_t nf4s_quantize(const float *x, int64_t n, int32_t block_size, uint8_t *pa
   hipLaunchKernelGGL(codes_generic_kernel, dim3(grid_for(npk, 256)), dim3(256), 0, s, x, n,
                      block_size, absmax, packed, npk);
   return check_launch("codes_generic_kernel");
+}
+
+int32_t nf4s_quantize_bf16(const uint16_t *x, int64_t n, int32_t block_size, uint8_t *packed,
+                           float *absmax, void *stream) {
+  if (n < 0) return fail(NF4S_ERR_INVALID_ARGUMENT, "negative element count");
+  if (block_size != 64)
+    return fail(NF4S_ERR_UNSUPPORTED_SHAPE, "bf16 quantize needs block_size 64, got %d",
+                block_size);
+  if (n == 0) return NF4S_OK;
+  if (x == nullptr || packed == nullptr || absmax == nullptr)
+    return fail(NF4S_ERR_INVALID_ARGUMENT, "NULL buffer");
+  const int64_t nb = (n + 63) / 64;
+  hipLaunchKernelGGL(quantize64_kernel<uint16_t>, dim3(grid_for((nb + 3) / 4, 1)), dim3(256), 0,
+                     as_stream(stream), x, n, packed, absmax, nb);
+  return check_launch("quantize64_kernel");
+}
+
+int32_t nf4s_quantize_dq(const float *x, int64_t n, int32_t block_size, int32_t group,
+                         uint8_t *packed, uint8_t *absmax_q, float *absmax_scale, void *stream) {
+  return quantize_dq<float>(x, n, block_size, group, packed, absmax_q, absmax_scale, stream);
+}
+
+int32_t nf4s_quantize_dq_bf16(const uint16_t *x, int64_t n, int32_t block_size, int32_t group,
+                              uint8_t *packed, uint8_t *absmax_q, float *absmax_scale,
+                              void *stream) {
+  return quantize_dq<uint16_t>(x, n, block_size, group, packed, absmax_q, absmax_scale, stream);
 }
 
 int32_t nf4s_dq_encode(const float *absmax, int64_t nblocks, int32_t group, uint8_t *q,

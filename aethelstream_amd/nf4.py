@@ -191,16 +191,43 @@ def quantize_nf4(tensor: torch.Tensor, block_size: int = BLOCK_SIZE) -> Nf4Resul
     if not tensor.is_cuda:
         raise ValueError("quantize_nf4 runs on the device: pass a cuda tensor")
     original_shape = list(tensor.shape)
-    flat = tensor.detach().float().contiguous().reshape(-1)
+    flat = _flat_input(tensor, block_size)
     n = flat.numel()
     packed = torch.empty((n + 1) // 2, dtype=torch.uint8, device=flat.device)
     absmax = torch.empty((n + block_size - 1) // block_size, dtype=torch.float32,
                          device=flat.device)
-    lib = _lib.load()
-    _lib.check(lib.nf4s_quantize(flat.data_ptr(), n, block_size, packed.data_ptr(),
-                                 absmax.data_ptr(), _stream_ptr(flat)))
+    _quantize_into(flat, block_size, packed, absmax)
     return Nf4Result(packed=packed, absmax=absmax, original_shape=original_shape,
                      block_size=block_size)
+
+
+def _flat_input(tensor: torch.Tensor, block_size: int) -> torch.Tensor:
+    """The values to quantize as a flat device tensor: bf16 is kept as is
+    (the kernels widen it exactly) when block_size is 64, anything else is
+    converted to fp32."""
+    t = tensor.detach()
+    if t.dtype == torch.bfloat16 and block_size == BLOCK_SIZE:
+        return t.contiguous().reshape(-1)
+    return t.float().contiguous().reshape(-1)
+
+
+def _quantize_into(flat: torch.Tensor, block_size: int, packed: torch.Tensor,
+                   absmax: torch.Tensor) -> None:
+    lib = _lib.load()
+    fn = lib.nf4s_quantize_bf16 if flat.dtype == torch.bfloat16 else lib.nf4s_quantize
+    _lib.check(fn(flat.data_ptr(), flat.numel(), block_size, packed.data_ptr(),
+                  absmax.data_ptr(), _stream_ptr(flat)))
+
+
+def _quantize_dq_into(flat: torch.Tensor, group: int, packed: torch.Tensor,
+                      q: torch.Tensor, scale: torch.Tensor) -> None:
+    lib = _lib.load()
+    fn = lib.nf4s_quantize_dq_bf16 if flat.dtype == torch.bfloat16 else lib.nf4s_quantize_dq
+    _lib.check(fn(flat.data_ptr(), flat.numel(), BLOCK_SIZE, group, packed.data_ptr(),
+                  q.data_ptr(), scale.data_ptr(), _stream_ptr(flat)))
+
+
+MAX_FUSED_DQ_GROUP = 8192   # nf4s_quantize_dq keeps a group's absmax in LDS
 
 
 def dq_encode(absmax: torch.Tensor, group: int = DQ_GROUP):
@@ -217,7 +244,21 @@ def dq_encode(absmax: torch.Tensor, group: int = DQ_GROUP):
 
 def quantize_weight(tensor: torch.Tensor, block_size: int = BLOCK_SIZE,
                     double_quant: bool = False, dq_group: int = DQ_GROUP) -> Nf4Weight:
-    """Quantize a weight into an :class:`Nf4Weight`, optionally double-quantized."""
+    """Quantize a weight into an :class:`Nf4Weight`, optionally double-quantized
+    (one fused launch for block 64 and groups up to MAX_FUSED_DQ_GROUP)."""
+    if (double_quant and block_size == BLOCK_SIZE and tensor.is_cuda
+            and 0 < dq_group <= MAX_FUSED_DQ_GROUP and dq_group & (dq_group - 1) == 0):
+        flat = _flat_input(tensor, block_size)
+        n = flat.numel()
+        nb = (n + block_size - 1) // block_size
+        packed = torch.empty((n + 1) // 2, dtype=torch.uint8, device=flat.device)
+        q = torch.empty(nb, dtype=torch.uint8, device=flat.device)
+        scale = torch.empty((nb + dq_group - 1) // dq_group, dtype=torch.float32,
+                            device=flat.device)
+        _quantize_dq_into(flat, dq_group, packed, q, scale)
+        return Nf4Weight(packed=packed, absmax=None, shape=list(tensor.shape),
+                         block_size=block_size, absmax_q=q, absmax_scale=scale,
+                         dq_group=dq_group)
     r = quantize_nf4(tensor, block_size)
     w = Nf4Weight(packed=r.packed, absmax=r.absmax, shape=r.original_shape,
                   block_size=block_size)
@@ -225,6 +266,32 @@ def quantize_weight(tensor: torch.Tensor, block_size: int = BLOCK_SIZE,
         q, s = dq_encode(r.absmax, dq_group)
         w = Nf4Weight(packed=r.packed, absmax=None, shape=r.original_shape,
                       block_size=block_size, absmax_q=q, absmax_scale=s, dq_group=dq_group)
+    return w
+
+
+def requantize_(w: Nf4Weight, values: torch.Tensor) -> Nf4Weight:
+    """Re-quantize `values` (fp32 or bf16, w.numel elements) into w's own
+    buffers on the device, with w's block size and double-quant group: the
+    weights an update step modified (doublepass/src/precision.rs:187-202)
+    before their write-back (FlowCast::on_weights_updated,
+    flowcast/src/lib.rs:501-521).  Allocates nothing on the device."""
+    if not values.is_cuda:
+        raise ValueError("requantize_ runs on the device: pass a cuda tensor")
+    if values.numel() != w.numel:
+        raise ValueError(f"requantize_ needs {w.numel} values, got {values.numel()}")
+    if not values.is_contiguous():
+        raise ValueError("requantize_ takes a contiguous tensor")
+    flat = values.detach().reshape(-1)
+    if not (flat.dtype == torch.bfloat16 and w.block_size == BLOCK_SIZE):
+        if flat.dtype != torch.float32:
+            raise ValueError("requantize_ takes float32 values (or bfloat16 for block 64)")
+    if w.double_quant:
+        if w.block_size != BLOCK_SIZE or w.dq_group > MAX_FUSED_DQ_GROUP:
+            raise ValueError("requantize_ of double-quantized weights needs block 64 and "
+                             f"dq_group <= {MAX_FUSED_DQ_GROUP}")
+        _quantize_dq_into(flat, w.dq_group, w.packed, w.absmax_q, w.absmax_scale)
+    else:
+        _quantize_into(flat, w.block_size, w.packed, w.absmax)
     return w
 
 

@@ -93,6 +93,30 @@ int32_t nf4s_dq_encode(const float *absmax, int64_t nblocks, int32_t group,
                        uint8_t *q, float *scale, void *stream);
 
 /*
+ * nf4s_quantize for bfloat16 input (each value widened exactly to fp32 first),
+ * block_size 64.  The weights a bf16 update leaves
+ * (doublepass/src/precision.rs:187-202) re-quantize without an fp32 copy.
+ */
+int32_t nf4s_quantize_bf16(const uint16_t *x, int64_t n, int32_t block_size,
+                           uint8_t *packed, float *absmax, void *stream);
+
+/*
+ * Quantize + double-quant in one launch (block_size 64, group a power of two
+ * <= 8192): packed codes, uint8 absmax codes and one fp32 scale per group,
+ * bit-identical to nf4s_quantize followed by nf4s_dq_encode, written into the
+ * caller's buffers without scratch memory.  For weights modified by the
+ * update step (doublepass/src/precision.rs:187-202) before their write-back
+ * (FlowCast::on_weights_updated, flowcast/src/lib.rs:501-521).
+ */
+int32_t nf4s_quantize_dq(const float *x, int64_t n, int32_t block_size,
+                         int32_t group, uint8_t *packed, uint8_t *absmax_q,
+                         float *absmax_scale, void *stream);
+int32_t nf4s_quantize_dq_bf16(const uint16_t *x, int64_t n, int32_t block_size,
+                              int32_t group, uint8_t *packed,
+                              uint8_t *absmax_q, float *absmax_scale,
+                              void *stream);
+
+/*
  * Dequantize n elements of `t` to IEEE binary16 (RNE).
  * Replaces dequant_nf4_into (shard_engine/src/nf4.rs:37-83): out[e] =
  * f16(code[nibble(e)] * absmax[e / block_size]), one fp32 multiply; fails

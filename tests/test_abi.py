@@ -76,3 +76,14 @@ def test_python_mirror_raises_malformed_index():
     with pytest.raises(ValueError):
         nf4.dequant_nf4_into(torch.zeros(4, dtype=torch.uint8), torch.ones(1),
                              torch.zeros(8, dtype=torch.float16), 64)
+
+
+def test_requantize_argument_rejection():
+    # Rejected before any launch: wrong block size, non-power-of-two group.
+    lib = _lib.load()
+    p = ctypes.c_void_p(16)
+    assert lib.nf4s_quantize_dq(p, 128, 32, 256, p, p, p, None) == _lib.NF4S_ERR_UNSUPPORTED_SHAPE
+    assert lib.nf4s_quantize_dq(p, 128, 64, 3, p, p, p, None) == _lib.NF4S_ERR_INVALID_ARGUMENT
+    assert lib.nf4s_quantize_dq_bf16(p, 128, 64, 16384, p, p, p, None) == _lib.NF4S_ERR_INVALID_ARGUMENT
+    assert lib.nf4s_quantize_bf16(p, 128, 32, p, p, None) == _lib.NF4S_ERR_UNSUPPORTED_SHAPE
+    assert lib.nf4s_quantize_dq(p, -1, 64, 256, p, p, p, None) == _lib.NF4S_ERR_INVALID_ARGUMENT
