@@ -211,18 +211,22 @@ template <bool kDQ>
 struct FwdProducer : FwdStore, PerStepLoads<kDQ, FwdProducer<kDQ>> {
   const uint8_t *ptr;   // packed bytes of (row, half) at step 0
   int64_t am_idx;       // absmax block index at step 0
-  __device__ void init(const GemmArgs &g, int64_t o0, uint32_t b0_lds) {
+  AbsmaxRef am;
+  // Tile row r takes W row n0 + r (n0 = the tile's first output column).
+  __device__ void init(const GemmArgs &g, int64_t n0, uint32_t b0_lds) {
     (void)b0_lds;
     init_row();
-    int64_t n = o0 + row;
+    int64_t n = n0 + row;
     if (n >= g.wn) n = g.wn - 1;  // ragged N: clamp (outputs are not stored)
     ptr = g.packed + n * (g.wk >> 1) + 16 * h;
     am_idx = n * (g.wk >> 6);
+    am = g.am;
   }
   __device__ __forceinline__ void load_step(const GemmArgs &g, int64_t step, u32x4 &w,
                                             AbsRaw &a) const {
+    (void)g;
     w = *reinterpret_cast<const u32x4 *>(ptr + step * 32);
-    a = absmax_load<kDQ>(g.am, am_idx + step);
+    a = absmax_load<kDQ>(am, am_idx + step);
   }
 };
 
@@ -250,15 +254,18 @@ struct FwdBatchProducer : FwdStore {
   u32x4 X[2], Y[2];
   typedef typename std::conditional<kDQ, u32x2, u32x4>::type Group;
   Group cur, nxt;  // kDQ: {codes of 4 blocks, scale bits}; else 4 fp32 absmax
+  AbsmaxRef am;
 
-  __device__ void init(const GemmArgs &g, int64_t o0, uint32_t b0_lds) {
+  // Tile row r takes W row n0 + r (n0 = the tile's first output column).
+  __device__ void init(const GemmArgs &g, int64_t n0, uint32_t b0_lds) {
     (void)b0_lds;
     init_row();
     const int lane = threadIdx.x & 63;
-    int64_t n = o0 + row;
+    int64_t n = n0 + row;
     if (n >= g.wn) n = g.wn - 1;
     am_idx = n * (g.wk >> 6);
-    int64_t nx = o0 + 32 * (threadIdx.x >> 6) + (lane & 15);
+    am = g.am;
+    int64_t nx = n0 + 32 * (threadIdx.x >> 6) + (lane & 15);
     int64_t ny = nx + 16;
     if (nx >= g.wn) nx = g.wn - 1;
     if (ny >= g.wn) ny = g.wn - 1;
@@ -272,12 +279,13 @@ struct FwdBatchProducer : FwdStore {
     y = *reinterpret_cast<const u32x4 *>(pky + p * 64);
   }
   __device__ __forceinline__ void load_group(const GemmArgs &g, int64_t gi, Group &v) const {
+    (void)g;
     const int64_t blk = am_idx + 4 * gi;
     if constexpr (kDQ) {
-      v.x = *reinterpret_cast<const uint32_t *>(g.am.q + blk);
-      v.y = __builtin_bit_cast(uint32_t, g.am.scale[blk >> g.am.group_shift]);
+      v.x = *reinterpret_cast<const uint32_t *>(am.q + blk);
+      v.y = __builtin_bit_cast(uint32_t, am.scale[blk >> am.group_shift]);
     } else {
-      v = *reinterpret_cast<const u32x4 *>(g.am.absmax + blk);
+      v = *reinterpret_cast<const u32x4 *>(am.absmax + blk);
     }
   }
   // The vector elements are copied to scalars before the bit casts:
@@ -369,6 +377,7 @@ struct DgradProducer : PerStepLoads<kDQ, DgradProducer<kDQ>> {
   int r, q;
   uint32_t valid_mask;  // all ones when the thread's columns exist
   uint32_t sbase[8];    // LDS byte addresses in weight buffer 0 (see above)
+  AbsmaxRef am;
   __device__ void init(const GemmArgs &g, int64_t o0, uint32_t b0_lds) {
     r = threadIdx.x >> 2;
     q = threadIdx.x & 3;
@@ -382,12 +391,13 @@ struct DgradProducer : PerStepLoads<kDQ, DgradProducer<kDQ>> {
     const int64_t c = valid ? col : 0;
     ptr = g.packed + (int64_t)r * (g.wk >> 1) + (c >> 1);
     am_idx = (int64_t)r * (g.wk >> 6) + (c >> 6);
+    am = g.am;
   }
   __device__ __forceinline__ void load_step(const GemmArgs &g, int64_t step, u32x4 &w,
                                             AbsRaw &a) const {
     // Step s covers W rows 64s .. 64s+63.
     w = *reinterpret_cast<const u32x4 *>(ptr + step * 64 * (g.wk >> 1));
-    a = absmax_load<kDQ>(g.am, am_idx + step * 64 * (g.wk >> 6));
+    a = absmax_load<kDQ>(am, am_idx + step * 64 * (g.wk >> 6));
   }
   // Columns beyond k read column 0's bytes and are zeroed via the absmax.
   __device__ __forceinline__ float masked(float a) const {
@@ -969,6 +979,91 @@ __global__ void __launch_bounds__(kGemmThreads, 1) nf4_gemm_fwd_kernel(const Gro
   }
 }
 
+// silu(x) = x / (1 + e^-x) (doublepass/src/math.rs:91-93) in fp32, with the
+// hardware base-2 exponential and reciprocal: x * rcp(1 + 2^(-x log2 e)).
+__device__ __forceinline__ float silu(float x) {
+  const float e = __builtin_amdgcn_exp2f(-x * 1.4426950408889634f);
+  return x * __builtin_amdgcn_rcpf(1.0f + e);
+}
+
+// SwiGLU epilogue: accumulator tiles nt = 0, 1 hold gate columns c0 + 32nt +
+// 8j + 4g + i, tiles nt + 2 the up columns with the same index (the weight
+// tile's rows 64-127 are the up rows), so hidden = silu(gate) * up is
+// elementwise within a lane.  Four adjacent hidden columns leave as one
+// 8-byte store.
+__device__ __forceinline__ void store_swiglu(const GemmArgs &g, const floatx16 (&acc)[4][4],
+                                             int64_t m0, int64_t c0, int jl, int grp) {
+  const bool vec_ok = ((reinterpret_cast<uintptr_t>(g.out) & 7) == 0) && ((g.ldo & 3) == 0);
+  const int64_t cl = g.O - (c0 + 4 * grp);
+  const int32_t clim = (int32_t)(cl < 0 ? 0 : (cl > (1 << 30) ? (1 << 30) : cl));
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) {
+    const int64_t m = m0 + 32 * mt + jl;
+    if (m < g.M) {
+      uint16_t *orow = g.out + m * g.ldo + c0 + 4 * grp;
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int c = 32 * nt + 8 * j;
+          float h[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            h[i] = silu(acc[mt][nt][4 * j + i]) * acc[mt][nt + 2][4 * j + i];
+          const uint32_t lo = pack_bf16x2(h[0], h[1]);
+          const uint32_t hi = pack_bf16x2(h[2], h[3]);
+          if (vec_ok && c + 4 <= clim) {
+            *reinterpret_cast<u32x2 *>(orow + c) = (u32x2){lo, hi};
+          } else {
+            if (c < clim) orow[c] = (uint16_t)(lo & 0xffffu);
+            if (c + 1 < clim) orow[c + 1] = (uint16_t)(lo >> 16);
+            if (c + 2 < clim) orow[c + 2] = (uint16_t)(hi & 0xffffu);
+            if (c + 3 < clim) orow[c + 3] = (uint16_t)(hi >> 16);
+          }
+        }
+    }
+  }
+}
+
+// Forward with the SwiGLU of single_layer_forward fused into the epilogue
+// (doublepass/src/forward.rs:251-254): hidden = silu(x . Wg^T) * (x . Wu^T).
+// A tile is 512 rows x 64 hidden columns c0..c0+63; its weight tile holds
+// gate rows c0..c0+63 (produced by waves 0-1) and up rows c0..c0+63 (waves
+// 2-3), so each tile does the MFMA work of a 128-column tile and writes half
+// the output bytes.  grp[0] is the gate weight, grp[1] the up weight.
+template <class Producer>
+__global__ void __launch_bounds__(kGemmThreads, 1) nf4_gemm_swiglu_kernel(const GroupedArgs ga) {
+  const int T = ga.base.tiles_m * ga.tiles_o;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int jl = lane & 31;
+  const int grp = lane >> 5;
+  const GemmGroup &gw = ga.grp[wave < 2 ? 0 : 1];
+#pragma unroll 1
+  for (int b = blockIdx.x; b < T; b += gridDim.x) {
+    const GemmArgs &g = ga.base;
+    int tm, th;
+    map_tile(b, g.tiles_m, ga.tiles_o, tm, th);
+    const int64_t m0 = (int64_t)tm * kTileM + wave * 128;
+    const int64_t c0 = (int64_t)th * (kTileO / 2);
+    uint32_t aoff[16];
+    const __amdgpu_buffer_rsrc_t arsrc = activation_setup(g, m0, lane, aoff);
+    // This wave's weight: tile rows 0-63 are gate rows c0 + r, rows 64-127
+    // up rows c0 + r - 64.
+    GemmArgs gp = g;
+    gp.packed = gw.packed;
+    gp.am = gw.am;
+    gp.wn = gw.wn;
+    Producer prod;
+    prod.init(gp, wave < 2 ? c0 : c0 - 64, (uint32_t)(uintptr_t)(lds_void_t *)&g_lds_b[0][0]);
+    floatx16 acc[4][4];
+    zero_acc(acc);
+    gemm_main<Producer>(g, prod, acc, &g_lds_a[wave][0][0], &g_lds_a[wave][1][0], g_lds_b[0],
+                        g_lds_b[1], arsrc, aoff, g.R / kStep, jl, grp);
+    store_swiglu(g, acc, m0, c0, jl, grp);
+  }
+}
+
 // Input gradient: dx = sum_i dy_i . W_i, the groups run one after another
 // into the same accumulator.  Between two groups no barrier is needed: every
 // read of the shared weight tiles ended before the last step's barrier, and
@@ -1159,6 +1254,55 @@ static int32_t gemm_fwd_groups(const uint16_t *x, const nf4s_tensor *ws, const i
   return NF4S_OK;
 }
 
+// hidden [m, ff] = silu(x . Wg^T) * (x . Wu^T), Wg and Wu [ff, k] of one kind.
+static int32_t gemm_swiglu(const uint16_t *x, const nf4s_tensor *wg, const nf4s_tensor *wu,
+                           int64_t m, int64_t ff, int64_t k, uint16_t *hidden, hipStream_t s) {
+  if (wg == nullptr || wu == nullptr)
+    return fail(NF4S_ERR_INVALID_ARGUMENT, "weight descriptor is NULL");
+  int32_t rc = check_gemm(x, wg, m, ff, k, hidden);
+  if (rc == NF4S_OK) rc = check_gemm(x, wu, m, ff, k, hidden);
+  if (rc == NF4S_OK) rc = check_offsets(k);
+  if (rc != NF4S_OK) return rc;
+  const bool dq = wg->absmax_q != nullptr;
+  const bool batch = fwd_batchable(*wg, k) && fwd_batchable(*wu, k);
+  if ((wu->absmax_q != nullptr) != dq)
+    return fail(NF4S_ERR_UNSUPPORTED_SHAPE,
+                "gate and up weights must both be double-quantized or both not");
+  if (m == 0) return NF4S_OK;
+  GroupedArgs ga{};
+  GemmArgs &g = ga.base;
+  g.a = x;
+  g.lda = k;
+  g.out = hidden;
+  g.ldo = ff;
+  g.M = m;
+  g.O = ff;
+  g.R = k;
+  g.wk = k;
+  g.tiles_m = (int32_t)((m + kTileM - 1) / kTileM);
+  const int64_t tiles_h = (ff + kTileO / 2 - 1) / (kTileO / 2);
+  if ((int64_t)g.tiles_m * tiles_h > 0x7fffffff)
+    return fail(NF4S_ERR_UNSUPPORTED_SHAPE, "too many tiles");
+  ga.tiles_o = (int32_t)tiles_h;
+  ga.grp[0] = group_of(*wg, ff);
+  ga.grp[1] = group_of(*wu, ff);
+  ga.ngroups = 2;
+  const uint32_t grid = persistent_grid((int64_t)g.tiles_m * tiles_h);
+  if (batch && dq)
+    hipLaunchKernelGGL(nf4_gemm_swiglu_kernel<FwdBatchProducer<true>>, dim3(grid),
+                       dim3(kGemmThreads), 0, s, ga);
+  else if (batch)
+    hipLaunchKernelGGL(nf4_gemm_swiglu_kernel<FwdBatchProducer<false>>, dim3(grid),
+                       dim3(kGemmThreads), 0, s, ga);
+  else if (dq)
+    hipLaunchKernelGGL(nf4_gemm_swiglu_kernel<FwdProducer<true>>, dim3(grid), dim3(kGemmThreads),
+                       0, s, ga);
+  else
+    hipLaunchKernelGGL(nf4_gemm_swiglu_kernel<FwdProducer<false>>, dim3(grid),
+                       dim3(kGemmThreads), 0, s, ga);
+  return check_launch("nf4_gemm_swiglu");
+}
+
 // Input gradient dx [m, k] = sum_i dy_i [m, ns[i]] . W_i [ns[i], k].
 static int32_t gemm_dgrad_groups(const uint16_t *const *dys, const nf4s_tensor *ws,
                                  const int64_t *ns, int32_t count, int64_t m, int64_t k,
@@ -1222,6 +1366,12 @@ int32_t nf4s_gemm_fwd_grouped(const uint16_t *x, const nf4s_tensor *ws, const in
                               uint16_t *const *ys, int32_t count, int64_t m, int64_t k,
                               void *stream) {
   return gemm_fwd_groups(x, ws, ns, ys, count, m, k, as_stream(stream));
+}
+
+int32_t nf4s_gemm_fwd_swiglu(const uint16_t *x, const nf4s_tensor *w_gate,
+                             const nf4s_tensor *w_up, int64_t m, int64_t ff, int64_t k,
+                             uint16_t *hidden, void *stream) {
+  return gemm_swiglu(x, w_gate, w_up, m, ff, k, hidden, as_stream(stream));
 }
 
 int32_t nf4s_gemm_dgrad_sum(const uint16_t *const *dys, const nf4s_tensor *ws, const int64_t *ns,

@@ -8,6 +8,8 @@
                  (doublepass/src/backward.rs:79-85,117-129,160-168,284-300).
 ``linear_fwd_grouped``  y_i = x . W_i^T for weights sharing x, one launch
                  (q/k/v at forward.rs:174-176, gate/up at forward.rs:251-252).
+``linear_swiglu``       hidden = silu(x . Wg^T) * (x . Wu^T), the SwiGLU of
+                 forward.rs:251-254 fused into the GEMM epilogue.
 ``linear_dgrad_sum``    dx = sum_i dy_i . W_i, one launch and one rounding
                  (d_h1 at backward.rs:284-300, d_h2 at backward.rs:117-129).
 
@@ -92,6 +94,24 @@ def linear_fwd_grouped(x: torch.Tensor, ws: Sequence[Nf4Weight],
     _lib.check(_lib.load().nf4s_gemm_fwd_grouped(x.data_ptr(), descs, ns, ys, len(ws), m, k,
                                                  _stream_ptr(x)))
     return list(outs)
+
+
+def linear_swiglu(x: torch.Tensor, w_gate: Nf4Weight, w_up: Nf4Weight,
+                  out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """hidden[M, ff] = silu(x . Wg^T) * (x . Wu^T) (forward.rs:251-254; silu_f,
+    math.rs:91-93): gate and up stay fp32 in the accumulators, hidden is bf16."""
+    ff, k = int(w_gate.shape[0]), int(w_gate.shape[1])
+    if [int(d) for d in w_up.shape] != [ff, k]:
+        raise ValueError("gate and up weights must have the same shape")
+    _check_act(x, k, "x")
+    m = x.shape[0]
+    if out is None:
+        out = torch.empty(m, ff, dtype=torch.bfloat16, device=x.device)
+    _check_act(out, ff, "out")
+    dg, du = w_gate.descriptor(), w_up.descriptor()
+    _lib.check(_lib.load().nf4s_gemm_fwd_swiglu(x.data_ptr(), ctypes.byref(dg), ctypes.byref(du),
+                                                m, ff, k, out.data_ptr(), _stream_ptr(x)))
+    return out
 
 
 def linear_dgrad_sum(dys: Sequence[torch.Tensor], ws: Sequence[Nf4Weight],

@@ -18,6 +18,10 @@ Under "stream", config 5: 80 70B layers in pinned host memory streamed
 through a two-slot device buffer (H2D on a copy stream) while the previous
 layer's forward GEMMs run, 4096 tokens: layers/s, H2D GB/s, overlap.
 
+Config 4 also reports the forward pass with SwiGLU fused into the gate/up
+epilogue (hidden = silu(x.Wg^T) * (x.Wu^T), forward.rs:251-254) next to the
+grouped gate/up launch that writes gate and up.
+
 Also under "gemm": "bf16_gemm_reference", a plain bf16 GEMM (torch.matmul,
 hipBLASLt) of the 70B gate shape on the same box, and what an unfused path
 (dequantize the layer to bf16, then that GEMM rate) would reach on config 4.
@@ -249,6 +253,20 @@ def bench_gemm(torch, nf4, gemm, args):
         md = timed(torch, lambda: gemm.linear_dgrad(dy, w, dx), steps4, 1)
         per[name] = {"fwd_tflops": round(f / (mf * 1e-3) / 1e12, 1),
                      "dgrad_tflops": round(f / (md * 1e-3) / 1e12, 1)}
+    # The first forward of a double-pass step only hands `hidden` to down:
+    # SwiGLU fused into the gate/up epilogue (forward.rs:251-254).
+    hsw = torch.empty(M, 28672, dtype=torch.bfloat16, device="cuda")
+
+    def fwd_pass_swiglu():
+        gemm.linear_fwd_grouped(h, ws[0:3], ys[0:3])
+        gemm.linear_fwd(h, ws[3], ys[3])
+        gemm.linear_swiglu(h, ws[4], ws[5], hsw)
+        gemm.linear_fwd(hsw, ws[6], ys[6])
+
+    ms_fs = timed(torch, fwd_pass_swiglu, steps4, 1)
+    fl_gu = 2 * 2.0 * M * 28672 * 8192
+    ms_gu = timed(torch, lambda: gemm.linear_fwd_grouped(h, ws[4:6], ys[4:6]), steps4, 1)
+    ms_sw = timed(torch, lambda: gemm.linear_swiglu(h, ws[4], ws[5], hsw), steps4, 1)
     tf_l = 3 * fl_pass / (ms_l * 1e-3) / 1e12
     res["config4_70b_layer"] = {
         "tflops": round(tf_l, 1), "ms_per_layer_step": round(ms_l, 3),
@@ -257,6 +275,9 @@ def bench_gemm(torch, nf4, gemm, args):
                     "summed, o, d_gate.Wg+d_up.Wu summed, down",
         "frac_of_bf16_peak": round(tf_l / BF16_PEAK_TFLOPS, 4),
         "fwd_pass_tflops": round(fl_pass / (ms_f * 1e-3) / 1e12, 1),
+        "fwd_pass_swiglu_tflops": round(fl_pass / (ms_fs * 1e-3) / 1e12, 1),
+        "gate_up_grouped_tflops": round(fl_gu / (ms_gu * 1e-3) / 1e12, 1),
+        "gate_up_swiglu_fused_tflops": round(fl_gu / (ms_sw * 1e-3) / 1e12, 1),
         "dgrad_pass_tflops": round(fl_pass / (ms_d * 1e-3) / 1e12, 1),
         "per_matrix": per,
     }

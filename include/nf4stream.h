@@ -176,6 +176,18 @@ int32_t nf4s_gemm_fwd_grouped(const uint16_t *x, const nf4s_tensor *ws,
                               void *stream);
 
 /*
+ * Forward with SwiGLU fused into the epilogue: hidden[m, ff] (bf16) =
+ * silu(x . Wg^T) * (x . Wu^T), the gate and up products in fp32 and never
+ * written out.  Replaces the gate/up matmul_tb calls and the elementwise
+ * silu * up of single_layer_forward (doublepass/src/forward.rs:251-254;
+ * silu_f at doublepass/src/math.rs:91-93).  Wg and Wu are [ff, k], both
+ * double-quantized or both not; requirements as nf4s_gemm_fwd.
+ */
+int32_t nf4s_gemm_fwd_swiglu(const uint16_t *x, const nf4s_tensor *w_gate,
+                             const nf4s_tensor *w_up, int64_t m, int64_t ff,
+                             int64_t k, uint16_t *hidden, void *stream);
+
+/*
  * Summed input gradient: dx[m,k] = sum_i dy_i[m, ns[i]] . W_i for `count`
  * (1..4) NF4 weights W_i [ns[i], k], one launch, one fp32 accumulator per
  * output element, one bf16 rounding.  Replaces the accumulating dY.W loops

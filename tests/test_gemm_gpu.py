@@ -267,3 +267,54 @@ def test_grouped_argument_errors():
         gemm.linear_fwd_grouped(x, [w] * 5)
     with pytest.raises(Exception, match="double-quantized"):
         gemm.linear_dgrad_sum([x, x], [w, wq])
+
+
+# SwiGLU fused into the forward epilogue: hidden = silu(x.Wg^T) * (x.Wu^T)
+# (forward.rs:251-254, silu_f at math.rs:91-93).
+
+def _silu(v):
+    v = np.asarray(v, np.float64)
+    return v / (1.0 + np.exp(-v))
+
+
+@pytest.mark.parametrize("m,ff,k", [(700, 300, 256), (513, 130, 320), (64, 64, 1024),
+                                    (1, 192, 512), (1024, 256, 768)])
+@pytest.mark.parametrize("dq", [False, True])
+def test_swiglu_small_vs_oracle(m, ff, k, dq):
+    wg = _weight(ff, k, 71 + ff + k, dq)
+    wu = _weight(ff, k, 72 + ff + k, dq)
+    x, xh = _act(m, k, 29 + m)
+    h = gemm.linear_swiglu(x, wg, wu)
+    torch.cuda.synchronize()
+    hh = h.float().cpu().numpy()
+    for f16, tol in ((True, TOL_REF), (False, TOL_SAME)):
+        gate = oracle.matmul_tb(xh, _deq_host(wg, f16=f16)).astype(np.float64)
+        up = oracle.matmul_tb(xh, _deq_host(wu, f16=f16)).astype(np.float64)
+        assert rel_l2(hh, _silu(gate) * up) <= tol
+
+
+def test_swiglu_70b_shape():
+    # BASELINE config 4 gate/up at 8192 tokens, double-quant.
+    m, ff, k = 8192, 28672, 8192
+    g = torch.Generator(device=DEV).manual_seed(12)
+    wg = nf4.quantize_weight(torch.randn(ff, k, device=DEV, generator=g) * 0.02, double_quant=True)
+    wu = nf4.quantize_weight(torch.randn(ff, k, device=DEV, generator=g) * 0.02, double_quant=True)
+    x = torch.randn(m, k, device=DEV, generator=g).to(torch.bfloat16)
+    h = gemm.linear_swiglu(x, wg, wu)
+    gate = x.float() @ nf4.dequant(wg).float().t()
+    up = x.float() @ nf4.dequant(wu).float().t()
+    ref = torch.nn.functional.silu(gate) * up
+    torch.cuda.synchronize()
+    err = ((h.float() - ref).norm() / ref.norm()).item()
+    assert err <= TOL_SAME, err
+    del wg, wu, x, h, gate, up, ref
+
+
+def test_swiglu_argument_errors():
+    w = _weight(128, 128, 2)
+    wq = _weight(128, 128, 3, dq=True)
+    x = torch.zeros(4, 128, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(Exception, match="double-quantized"):
+        gemm.linear_swiglu(x, w, wq)
+    with pytest.raises(ValueError):
+        gemm.linear_swiglu(x, w, _weight(64, 128, 4))
