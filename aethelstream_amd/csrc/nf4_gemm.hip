@@ -26,6 +26,7 @@
 // accumulator layout is lane l: column l % 32, row 8(v/4) + 4g + v%4; the
 // weight fragment is the first operand, so the accumulator's columns are
 // activation rows and its rows are output columns.
+#include <atomic>
 #include <type_traits>
 
 #include "abi_common.hpp"
@@ -1166,17 +1167,19 @@ static GemmGroup group_of(const nf4s_tensor &w, int64_t wn) {
 // tiles.  The CU count is read once per device; a multiple of 8 keeps tile
 // b on XCD b % 8 (map_tile).
 static uint32_t persistent_grid(int64_t tiles) {
-  static int cus[64] = {0};
+  static std::atomic<int> cus[64];  // zero-initialized (static storage)
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-  if (cus[dev] == 0) {
+  int c = cus[dev].load(std::memory_order_relaxed);
+  if (c == 0) {
     int n = 0;
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         n <= 0)
       n = 256;
-    cus[dev] = (n + 7) & ~7;
+    c = (n + 7) & ~7;
+    cus[dev].store(c, std::memory_order_relaxed);  // every caller stores the same value
   }
-  return (uint32_t)(tiles < cus[dev] ? tiles : cus[dev]);
+  return (uint32_t)(tiles < c ? tiles : c);
 }
 
 template <class Producer>
