@@ -35,6 +35,7 @@
 namespace nf4s {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef short v4i16 __attribute__((ext_vector_type(4)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr int kGemmThreads = 256;
@@ -177,18 +178,17 @@ struct FwdStore {
     h = (lane >> 4) & 1;
   }
   __device__ __forceinline__ float masked(float a) const { return a; }
-  // The 8 elements of a word in natural order: out[j] = elements 2j, 2j+1.
-  static __device__ __forceinline__ void merge(const WordLookup &x, uint32_t out[4]) {
-    word_merge(x, out);
-  }
-  // Writes the 8 dequantized elements of packed word k in `part` of
-  // kStoreParts.
-  static constexpr int kStoreParts = 1;
+  // Writes the 8 dequantized elements of packed word k (natural order).
   template <int kPar, int k, int kPart>
   __device__ __forceinline__ void store(u32x4 *lds, const uint32_t out[4]) const {
     u32x4 v;
     v.x = out[0]; v.y = out[1]; v.z = out[2]; v.w = out[3];
     lds[lds_unit_b(row, 4 * h + k)] = v;
+  }
+  // Fragment j of sub-step s: tile rows 32j + jl, reduction unit 2s + grp.
+  __device__ __forceinline__ void read_b(const u32x4 *Bcur, u32x4 &out, int s, int j, int jl,
+                                         int grp) const {
+    out = Bcur[lds_unit_b(32 * j + jl, 2 * s + grp)];
   }
   // Whole-tile store (prologue).
   __device__ __forceinline__ void store_tile(u32x4 *lds, const u32x4 &w, float am) const {
@@ -357,41 +357,50 @@ struct FwdBatchProducer : FwdStore {
 
 // Dgrad producer: the step covers W rows n0..n0+63 (the reduction) and W
 // columns o0..o0+127 (the output).  Thread -> (W row r = tid/4, quarter
-// q = tid%4): 32 consecutive columns of one block.  The LDS tile is stored
-// transposed (LDS row = output column, 64 reduction values per row), so
-// each element is written as one 16-bit value.
+// q = tid%4): 32 consecutive columns of one block, dequantized as 4 words of
+// 8 elements and written as 4 16-B units.  The LDS tile keeps W's layout:
+// row r (256 B) holds the tile's 128 columns, unit u (columns 8u..8u+7) at
+// physical unit u ^ 5(r % 4).
 //
-// With col = 32q + 8k + j (packed word k, element j), the byte address of
-// element (col, r) in the weight tile (lds_unit_b) is
-//   (8k + j) * 128 + sbase[j ^ (k & 1)],
-//   sbase[c] = 4096q + 16 * ((r / 8) ^ 2q ^ c) + 2 * (r % 8),
-// so each store is one of 8 per-thread addresses plus an immediate offset.
-// The stores are written as inline asm: the compiler then does not treat
-// them as LDS accesses that may alias the activation DMAs in flight (it
-// would wait for those, vmcnt(0), before every store).  Their completion is
-// covered by the explicit lgkmcnt(0) before each step's barrier.
+// The MFMA fragment of output column o holds 8 consecutive reduction values,
+// a column of this tile.  ds_read_b64_tr_b16 transposes 4 x 4 blocks of
+// 16-bit values within each 16-lane group: lane i of the group receives
+// element i % 4 of the 8 bytes addressed by lane 4e + i / 4, e = 0..3.  So
+// when lane 4e + c addresses row e, columns 4c..4c+3 of a 16-column strip,
+// lane i receives column i of rows 0..3, and two such reads (rows 0-3, 4-7)
+// make the fragment.
+//
+// Banks (64 x 4 B): a 16-lane group of the ds_write_b128 covers rows with
+// c = r % 4 = 0..3 at quarters 0..3 and one word k, physical units
+// 4(q ^ c) + (k ^ c), 16 distinct; a 32-lane half of a transposed read
+// covers c = 0..3 at units 4j..4j+3 (fragment j), physical units
+// 4(j ^ c) + (u % 4 ^ c), 16 distinct.
 template <bool kDQ>
 struct DgradProducer : PerStepLoads<kDQ, DgradProducer<kDQ>> {
   static constexpr bool kFwd = false;
   const uint8_t *ptr;
   int64_t am_idx;
-  int r, q;
   uint32_t valid_mask;  // all ones when the thread's columns exist
-  uint32_t sbase[8];    // LDS byte addresses in weight buffer 0 (see above)
+  int sidx[4];          // LDS unit of the thread's word k
+  uint32_t roff[4];     // byte offset of the lane's read of fragment j (rows 0-3 of sub-step 0)
   AbsmaxRef am;
   __device__ void init(const GemmArgs &g, int64_t o0, uint32_t b0_lds) {
-    r = threadIdx.x >> 2;
-    q = threadIdx.x & 3;
+    (void)b0_lds;
+    const int r = threadIdx.x >> 2, q = threadIdx.x & 3, c = r & 3;
 #pragma unroll
-    for (int c = 0; c < 8; ++c)
-      sbase[c] = b0_lds + 4096u * (uint32_t)q + 16u * (uint32_t)((r >> 3) ^ (2 * q) ^ c) +
-                 2u * (uint32_t)(r & 7);
+    for (int k = 0; k < 4; ++k) sidx[k] = 16 * r + 4 * (q ^ c) + (k ^ c);
+    const int lane = threadIdx.x & 63, l16 = lane & 15, cr = l16 >> 2;
+    const int ub = 2 * ((lane >> 4) & 1) + ((l16 >> 1) & 1);  // unit within the fragment's 4
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      roff[j] = (uint32_t)(256 * (8 * (lane >> 5) + cr) + 16 * (4 * (j ^ cr) + (ub ^ cr)) +
+                           8 * (l16 & 1));
     const int64_t col = o0 + 32 * q;
     const bool valid = col < g.wk;
     valid_mask = valid ? 0xffffffffu : 0u;
-    const int64_t c = valid ? col : 0;
-    ptr = g.packed + (int64_t)r * (g.wk >> 1) + (c >> 1);
-    am_idx = (int64_t)r * (g.wk >> 6) + (c >> 6);
+    const int64_t cc = valid ? col : 0;
+    ptr = g.packed + (int64_t)r * (g.wk >> 1) + (cc >> 1);
+    am_idx = (int64_t)r * (g.wk >> 6) + (cc >> 6);
     am = g.am;
   }
   __device__ __forceinline__ void load_step(const GemmArgs &g, int64_t step, u32x4 &w,
@@ -404,28 +413,26 @@ struct DgradProducer : PerStepLoads<kDQ, DgradProducer<kDQ>> {
   __device__ __forceinline__ float masked(float a) const {
     return __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, a) & valid_mask);
   }
-  // Elements are stored one by one, so the pairs of the first merge half
-  // suffice: element j is half (j >> 1) & 1 of out[(j & 1) + 2 * (j >> 2)].
-  static __device__ __forceinline__ void merge(const WordLookup &x, uint32_t out[4]) {
-    word_pairs(x, out);
-  }
-  // Writes the 8 elements of packed word k as 16-bit values down 8 LDS rows
-  // (output columns); part p of 4 writes elements 2p and 2p+1.
-  // Weight buffer kPar (0 or 1, 16 KB apart) is the destination.
-  static constexpr int kStoreParts = 4;
+  // Writes the 8 dequantized elements of packed word k (natural order).
   template <int kPar, int k, int kPart>
   __device__ __forceinline__ void store(u32x4 *lds, const uint32_t out[4]) const {
-    (void)lds;
-    static_for<0, 2>([&](auto JJ) {
-      constexpr int j = 2 * kPart + decltype(JJ)::value;
-      constexpr int off = kPar * 16384 + (8 * k + j) * 128;
-      const uint32_t pr = out[(j & 1) + 2 * (j >> 2)];
-      const uint32_t a = sbase[j ^ (k & 1)];
-      if constexpr (((j >> 1) & 1) == 0)
-        asm volatile("ds_write_b16 %0, %1 offset:%2" ::"v"(a), "v"(pr), "i"(off) : "memory");
-      else
-        asm volatile("ds_write_b16_d16_hi %0, %1 offset:%2" ::"v"(a), "v"(pr), "i"(off) : "memory");
-    });
+    u32x4 v;
+    v.x = out[0]; v.y = out[1]; v.z = out[2]; v.w = out[3];
+    lds[sidx[k]] = v;
+  }
+  // Fragment j of sub-step s: output columns 32j + lane % 32, reduction rows
+  // 16s + 8(lane / 32) + 0..7.
+  __device__ __forceinline__ void read_b(const u32x4 *Bcur, u32x4 &out, int s, int j, int jl,
+                                         int grp) const {
+    (void)jl;
+    (void)grp;
+    typedef __attribute__((address_space(3))) char lds_char_t;
+    typedef __attribute__((address_space(3))) v4i16 lds_v4i16_t;
+    lds_char_t *base = (lds_char_t *)const_cast<u32x4 *>(Bcur) + roff[j] + 4096 * s;
+    const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t *)base);
+    const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t *)(base + 1024));
+    const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+    out = (u32x4){l2.x, l2.y, h2.x, h2.y};
   }
   __device__ __forceinline__ void store_tile(u32x4 *lds, const u32x4 &w, float am) const {
     const Lut16 lut = make_lut<false>(am);
@@ -437,11 +444,8 @@ struct DgradProducer : PerStepLoads<kDQ, DgradProducer<kDQ>> {
       word_select(words[k], x);
       word_even(lut, x);
       word_odd(lut, x);
-      word_pairs(x, o);
+      word_merge(x, o);
       this->template store<0, k, 0>(lds, o);
-      this->template store<0, k, 1>(lds, o);
-      this->template store<0, k, 2>(lds, o);
-      this->template store<0, k, 3>(lds, o);
     });
   }
 };
@@ -502,17 +506,17 @@ __device__ __forceinline__ void pin(float &x) { asm volatile("" : "+v"(x)); }
 
 // Fragment read k (0..7) of sub-step s into register buffer n, in the order
 // the sub-step's first MFMAs consume them: A0, B0, B1, B2, B3, A1, A2, A3.
-// Fragment j of A (B) holds rows 32j + jl of the activation (weight) tile.
-__device__ __forceinline__ void read_frag(const u32x4 *__restrict__ Acur,
+// Fragment j of A holds rows 32j + jl of the activation tile; fragment j of
+// B output columns 32j + jl of the weight tile (the producer's read_b).
+template <class Producer>
+__device__ __forceinline__ void read_frag(const Producer &prod, const u32x4 *__restrict__ Acur,
                                           const u32x4 *__restrict__ Bcur, u32x4 (&a)[2][4],
                                           u32x4 (&b)[2][4], int s, int k, int n, int jl, int grp) {
-  const int u = 2 * s + grp;
   if (k == 0 || k >= 5) {
     const int j = (k == 0) ? 0 : k - 4;
-    a[n][j] = Acur[lds_unit(32 * j + jl, u)];
+    a[n][j] = Acur[lds_unit(32 * j + jl, 2 * s + grp)];
   } else {
-    const int j = k - 1;
-    b[n][j] = Bcur[lds_unit_b(32 * j + jl, u)];
+    prod.read_b(Bcur, b[n][k - 1], s, k - 1, jl, grp);
   }
 }
 
@@ -522,41 +526,28 @@ __device__ __forceinline__ void read_frag(const u32x4 *__restrict__ Acur,
 //      'n' is R plus an N job
 //   L  one half-quarter of the product table (2 products, 1 conversion)
 //   W  one lookup stage of a packed word, in order: selectors, masks, even
-//      elements, odd elements, pairs and (forward only) natural order plus
-//      the 16-B store
+//      elements, odd elements, pairs, then natural order and the 16-B store
 //   N  one activation DMA of the NEXT step's tile, rows 64-127, into the
 //      other buffer
 //   A  one activation DMA of the step after next (t+2), rows 0-63, into the
 //      current buffer once this wave's reads of it have returned
-// In the dgrad plan some N/A slots also carry a P job: half of one word's
-// 16-bit transposed stores (dgrad_p_slot).  Each slot holds about the issue
-// time of one MFMA (32 cycles), and the 16 DMAs are spread over the step so
-// that the four waves of a CU never flood its texture-address unit (all 16
-// in the second half of the step, with 16 exempt at the barrier, measured
-// 5-9 % slower).  The barrier exempts the 8 A jobs.
+// Each slot holds about the issue time of one MFMA (32 cycles), and the 16
+// DMAs are spread over the step so that the four waves of a CU never flood
+// its texture-address unit (all 16 in the second half of the step, with 16
+// exempt at the barrier, measured 5-9 % slower).  The barrier exempts the 8
+// A jobs.  The dgrad plan is the same: its B fragment reads (two transposed
+// 8-byte reads each) sit in the same R slots.
 constexpr int kDmaInFlight = 8;
 constexpr char kPlanFwd[57] =
     "RnRnLLNLLNLLNLLN"
     "RnRnWWWWWWWWWWWW"
     "RRRRWWAWWAWWAWWA"
     "WWAWAWAA";
-constexpr char kPlanDgrad[57] =
-    "RRRRLNLLNLLNLLNL"
-    "RRRRWNWWNWWNWWNW"
-    "RRRRWWWWAWWAWWAW"
-    "AWAWAWAA";
-constexpr bool dgrad_p_slot(int n) {
-  return n == 27 || n == 30 || n == 40 || n == 43 || n == 46 || n == 48 || n == 54 || n == 55;
-}
+constexpr const char *kPlanDgrad = kPlanFwd;
 // Number of jobs of kind c before slot n ('n' counts as N).
 constexpr int plan_index(const char *plan, int n, char c) {
   int k = 0;
   for (int i = 0; i < n; ++i) k += (plan[i] == c) || (c == 'N' && plan[i] == 'n');
-  return k;
-}
-constexpr int p_index(int n) {
-  int k = 0;
-  for (int i = 0; i < n; ++i) k += dgrad_p_slot(i);
   return k;
 }
 
@@ -587,7 +578,7 @@ __device__ __forceinline__ void gemm_step(const GemmArgs &g, Producer &prod,
                                           int64_t t, int64_t nsteps, int jl, int grp) {
   constexpr int kPar = 1 - (kPhase & 1);
   constexpr bool kFwd = Producer::kFwd;
-  constexpr int kWordStages = kFwd ? 6 : 5;
+  constexpr int kWordStages = 6;
   const int64_t t1 = (t + 1 < nsteps) ? t + 1 : nsteps - 1;
   const int64_t t2 = (t + 2 < nsteps) ? t + 2 : nsteps - 1;
   Lut16 lut;
@@ -607,7 +598,7 @@ __device__ __forceinline__ void gemm_step(const GemmArgs &g, Producer &prod,
     acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
         __builtin_bit_cast(bf16x8, b[1][nt]), __builtin_bit_cast(bf16x8, a[1][mt]),
         acc[mt][nt], 0, 0, 0);
-    read_frag(Acur, Bcur, a, b, 0, i, 0, jl, grp);
+    read_frag(prod, Acur, Bcur, a, b, 0, i, 0, jl, grp);
     if constexpr (i == 3) prod.template issue_loads<kPhase>(g, t, nsteps);
     if constexpr (i == 5) prod.template prepare<kPhase>();
     if constexpr (i == 6) ta = prod.template table_absmax<kPhase>();
@@ -622,8 +613,8 @@ __device__ __forceinline__ void gemm_step(const GemmArgs &g, Producer &prod,
         __builtin_bit_cast(bf16x8, b[s & 1][nt]), __builtin_bit_cast(bf16x8, a[s & 1][mt]),
         acc[mt][nt], 0, 0, 0);
     if constexpr (kind == 'R' || kind == 'n') {
-      read_frag(Acur, Bcur, a, b, s + 1, 2 * i, (s + 1) & 1, jl, grp);
-      read_frag(Acur, Bcur, a, b, s + 1, 2 * i + 1, (s + 1) & 1, jl, grp);
+      read_frag(prod, Acur, Bcur, a, b, s + 1, 2 * i, (s + 1) & 1, jl, grp);
+      read_frag(prod, Acur, Bcur, a, b, s + 1, 2 * i + 1, (s + 1) & 1, jl, grp);
     }
     if constexpr (kind == 'N' || kind == 'n')
       dma(Aoth, 8 + plan_index(kFwd ? kPlanFwd : kPlanDgrad, n, 'N'), t1);
@@ -674,12 +665,6 @@ __device__ __forceinline__ void gemm_step(const GemmArgs &g, Producer &prod,
         pairs_merge(wp[k], o);
         prod.template store<kPar, k, 0>(Bnext, o);
       }
-    }
-    if constexpr (!kFwd && dgrad_p_slot(n)) {
-      constexpr int j = p_index(n);
-      constexpr int k = j >> 1, half = j & 1;
-      prod.template store<kPar, k, 2 * half>(Bnext, wp[k]);
-      prod.template store<kPar, k, 2 * half + 1>(Bnext, wp[k]);
     }
     __builtin_amdgcn_sched_barrier(0);
   });
