@@ -221,9 +221,9 @@ __global__ void __launch_bounds__(256) quantize_dq_kernel(const T *__restrict__ 
 
 constexpr int kMaxBatch = 16;
 constexpr int32_t kMaxDqGroup = 8192;  // quantize_dq_kernel keeps a group's absmax in LDS
-constexpr int kDqThreads = 256;                   // 4 waves
-constexpr int kDqRounds = 2;                      // rounds of 64 chunks per wave
-constexpr int64_t kTileChunks = 4LL * 64 * kDqRounds;
+constexpr int kDqWaves = 2;                        // waves per workgroup
+constexpr int kDqThreads = 64 * kDqWaves;
+constexpr int64_t kTileChunks = 64 * kDqWaves;     // one 32-element chunk per lane
 
 struct DqEntry {
   const uint8_t *packed;
@@ -240,16 +240,21 @@ struct DqBatch {
 };
 
 // One chunk = 32 elements = 16 B of packed nibbles -> 64 B of output, all in
-// one absmax block (block_size % 32 == 0).  A wave takes 64 consecutive
-// chunks per round: each lane loads one 16-B chunk (a coalesced 1 KB per
-// wave), builds that block's product table, dequantizes into LDS, and the
-// wave then writes the round's 4 KB of output as four contiguous 1 KB stores.
-// Scattered 16-B stores at a 64-B stride measured 7x slower on MI355X than
-// these contiguous ones.  The next round's chunk is loaded before the
-// current one is dequantized.
+// one absmax block (block_size % 32 == 0).  Each wave takes 64 consecutive
+// chunks: each lane loads one 16-B chunk (a coalesced 1 KB per wave), builds
+// that block's product table and dequantizes into LDS, and the wave then
+// writes its 4 KB of output as four contiguous 1 KB stores.  Scattered 16-B
+// stores at a 64-B stride measured 7x slower on MI355X than these contiguous
+// ones.
+// Small one-shot workgroups (2 waves, 8 KB of output, consecutive workgroups
+// on consecutive XCDs) keep the HBM write stream fastest: on MI355X this
+// shape measured 6.13 TB/s against 5.75 TB/s for 4-wave workgroups whose
+// waves each dequantized two rounds (32 KB per workgroup), and a write-only
+// fill shows the same preference (6.5 TB/s at 4 KB per workgroup, 5.3 TB/s
+// at 64 KB).
 template <bool kF16>
 __global__ void __launch_bounds__(kDqThreads) dequant_fast_kernel(const DqBatch batch) {
-  __shared__ u32x4 stage[4][64 * 4 + 4];  // per wave 4 KB, +1 pad unit per 16 lanes
+  __shared__ u32x4 stage[kDqWaves][64 * 4 + 4];  // per wave 4 KB, +1 pad unit per 16 lanes
   const int64_t tile = blockIdx.x;
   int idx = 0;
 #pragma unroll 1
@@ -258,52 +263,32 @@ __global__ void __launch_bounds__(kDqThreads) dequant_fast_kernel(const DqBatch 
   const DqEntry &E = batch.e[idx];
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
+  const int64_t cbase = (tile - E.tile_begin) * kTileChunks + wave * 64;
+  const int64_t nchunks = E.nchunks;
+  if (cbase >= nchunks) return;  // wave-uniform
   const u32x4 *src = reinterpret_cast<const u32x4 *>(E.packed);
   u32x4 *dst = reinterpret_cast<u32x4 *>(E.out);
-  const int64_t cw = ((tile - E.tile_begin) * 4 + wave) * 64 * kDqRounds;
-  const int64_t nchunks = E.nchunks;
-  const int32_t bs = E.block_size;
-
-  u32x4 w = {0u, 0u, 0u, 0u};
-  float am = 0.0f;
-  if (cw + lane < nchunks) {
-    w = __builtin_nontemporal_load(src + cw + lane);
-    am = load_absmax(E.am, ((cw + lane) * 32) / bs);
-  }
-#pragma unroll 1
-  for (int r = 0; r < kDqRounds; ++r) {
-    const int64_t cbase = cw + (int64_t)r * 64;
-    if (cbase >= nchunks) break;  // wave-uniform
-    const int64_t c = cbase + lane;
-    u32x4 wn = {0u, 0u, 0u, 0u};
-    float amn = 0.0f;
-    if (r + 1 < kDqRounds && c + 64 < nchunks) {
-      wn = __builtin_nontemporal_load(src + c + 64);
-      amn = load_absmax(E.am, ((c + 64) * 32) / bs);
-    }
-    if (c < nchunks) {
-      const Lut16 lut = make_lut<kF16>(am);
-      const uint32_t words[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        uint32_t o[4];
-        lut_apply8(lut, words[k], o);
-        u32x4 v;
-        v.x = o[0]; v.y = o[1]; v.z = o[2]; v.w = o[3];
-        const int u = lane * 4 + k;  // 16-B unit of the wave's 4 KB
-        stage[wave][u + (u >> 6)] = v;
-      }
-    }
-    __builtin_amdgcn_wave_barrier();
+  const int64_t c = cbase + lane;
+  if (c < nchunks) {
+    const u32x4 w = __builtin_nontemporal_load(src + c);
+    const Lut16 lut = make_lut<kF16>(load_absmax(E.am, (c * 32) / E.block_size));
+    const uint32_t words[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      const int u = k * 64 + lane;
-      if (cbase + (u >> 2) < nchunks)
-        __builtin_nontemporal_store(stage[wave][u + (u >> 6)], dst + cbase * 4 + u);
+      uint32_t o[4];
+      lut_apply8(lut, words[k], o);
+      u32x4 v;
+      v.x = o[0]; v.y = o[1]; v.z = o[2]; v.w = o[3];
+      const int u = lane * 4 + k;  // 16-B unit of the wave's 4 KB
+      stage[wave][u + (u >> 6)] = v;
     }
-    __builtin_amdgcn_wave_barrier();
-    w = wn;
-    am = amn;
+  }
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int u = k * 64 + lane;
+    if (cbase + (u >> 2) < nchunks)
+      __builtin_nontemporal_store(stage[wave][u + (u >> 6)], dst + cbase * 4 + u);
   }
 }
 
