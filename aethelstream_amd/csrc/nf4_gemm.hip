@@ -499,10 +499,6 @@ __device__ __forceinline__ void step_barrier() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
-// Makes x opaque at this point of the instruction stream: arithmetic that
-// uses it cannot be scheduled before the (volatile, ordered) empty asm.
-__device__ __forceinline__ void pin(uint32_t &x) { asm volatile("" : "+v"(x)); }
-__device__ __forceinline__ void pin(float &x) { asm volatile("" : "+v"(x)); }
 
 // Fragment read k (0..7) of sub-step s into register buffer n, in the order
 // the sub-step's first MFMAs consume them: A0, B0, B1, B2, B3, A1, A2, A3.
@@ -524,25 +520,34 @@ __device__ __forceinline__ void read_frag(const Producer &prod, const u32x4 *__r
 // sub-step 3 has 8 slots before the barrier, so a step has 56.  Job kinds:
 //   R  two fragment reads of the next sub-step (slots 0-3 of sub-steps 0-2);
 //      'n' is R plus an N job
-//   L  one half-quarter of the product table (2 products, 1 conversion)
+//   M  one quarter of the product table (4 products, 2 conversions, the
+//      quarter's two low/high byte words)
 //   W  one lookup stage of a packed word, in order: selectors, masks, even
 //      elements, odd elements, pairs, then natural order and the 16-B store
 //   N  one activation DMA of the NEXT step's tile, rows 64-127, into the
 //      other buffer
 //   A  one activation DMA of the step after next (t+2), rows 0-63, into the
 //      current buffer once this wave's reads of it have returned
-// Each slot holds about the issue time of one MFMA (32 cycles), and the 16
-// DMAs are spread over the step so that the four waves of a CU never flood
-// its texture-address unit (all 16 in the second half of the step, with 16
-// exempt at the barrier, measured 5-9 % slower).  The barrier exempts the 8
-// A jobs.  The dgrad plan is the same: its B fragment reads (two transposed
-// 8-byte reads each) sit in the same R slots.
+//   .  the MFMA alone
+// Each slot holds about the issue time of one MFMA (32 cycles).  The last
+// weight-tile store (word 3's W stage 5) sits at slot 43, 12 slots before
+// the barrier, whose lgkmcnt(0) must see it complete; the A jobs follow in
+// the last 12 slots, after a wait for this wave's fragment reads only (the
+// LDS queue is in order, so the wait exempts the stores issued after the
+// last R slot).  N jobs go early: the barrier exempts only the 8 A jobs.
+// On MI355X this plan measured +1.3 % (70B gate forward) to +3 % (70B q
+// input gradient) over one that stored the last word two slots before the
+// barrier; the 16 DMAs all in the second half of the step (16 exempt at the
+// barrier) measured 5-9 % slower, and the N jobs right after the barrier
+// 3-4 % slower for the input gradient.  The input-gradient plan is the same:
+// its B fragment reads (two transposed 8-byte reads each) sit in the same R
+// slots.
 constexpr int kDmaInFlight = 8;
 constexpr char kPlanFwd[57] =
-    "RnRnLLNLLNLLNLLN"
+    "RnRnMMNMMNWWWWNN"
     "RnRnWWWWWWWWWWWW"
-    "RRRRWWAWWAWWAWWA"
-    "WWAWAWAA";
+    "RRRRWWWWWWWW.A.A"
+    ".AAAAAA.";
 constexpr const char *kPlanDgrad = kPlanFwd;
 // Number of jobs of kind c before slot n ('n' counts as N).
 constexpr int plan_index(const char *plan, int n, char c) {
@@ -550,6 +555,36 @@ constexpr int plan_index(const char *plan, int n, char c) {
   for (int i = 0; i < n; ++i) k += (plan[i] == c) || (c == 'N' && plan[i] == 'n');
   return k;
 }
+// Weight-tile stores (W stage 5) issued after the plan's last R slot before
+// slot n: the LDS operations a wait for the fragment reads may leave pending.
+constexpr int stores_after_reads(const char *plan, int n) {
+  int last_r = -1;
+  for (int i = 0; i < n; ++i)
+    if (plan[i] == 'R' || plan[i] == 'n') last_r = i;
+  int stores = 0, j = 0;
+  for (int i = 0; i < n; ++i)
+    if (plan[i] == 'W') {
+      if (i > last_r && j % 6 == 5) ++stores;
+      ++j;
+    }
+  return stores;
+}
+// Shape of a plan: 56 slots; R/n at slots 0-3 of sub-steps 0-2; 8 N, 8 A, 24
+// W and 4 M jobs; the product table complete before the first lookup stage
+// that reads it (W stage 2 of word 0).
+constexpr bool plan_ok(const char *plan) {
+  int r = 0, w = 0;
+  for (int i = 0; i < 56; ++i) {
+    const bool rs = plan[i] == 'R' || plan[i] == 'n';
+    if (rs != (i < 48 && i % 16 < 4)) return false;
+    r += rs;
+    if (plan[i] == 'W' && w++ == 2 && plan_index(plan, i, 'M') != 4) return false;
+  }
+  return plan[56] == 0 && r == 12 && plan_index(plan, 56, 'N') == 8 &&
+         plan_index(plan, 56, 'A') == 8 && w == 24 && plan_index(plan, 56, 'M') == 4;
+}
+static_assert(plan_ok(kPlanFwd), "forward slot plan");
+static_assert(plan_ok(kPlanDgrad), "input-gradient slot plan");
 
 // One 64-deep reduction step t: 4 sub-steps of 16 MFMAs over the activation
 // tile in Acur (this wave's 128 rows) and the weight tile in Bcur.  Alongside
@@ -563,7 +598,11 @@ constexpr int plan_index(const char *plan, int n, char c) {
 // the barrier waits for all but the kDmaInFlight (8) most recent
 // vector-memory operations.
 // A wave issues in order, so other work only overlaps the matrix pipe when
-// it sits between MFMAs; sched_barrier fences keep the slot plan's order.
+// it sits between MFMAs; a sched_barrier fence after every slot keeps the
+// plan's order.  (Empty asm statements that pinned each stage's inputs to
+// its slot cost a hazard s_nop each and a register copy per table quarter,
+// 40 nops and 11 moves per step; without them the stages stay in their
+// slots and the step measured 0.4-1.3 % faster.)
 //
 // The step's barrier comes after MFMA 7 of sub-step 3.  The last 8 MFMAs
 // (a[1][2..3] x b[1][0..3], operands already in registers) open the NEXT
@@ -619,49 +658,35 @@ __device__ __forceinline__ void gemm_step(const GemmArgs &g, Producer &prod,
     if constexpr (kind == 'N' || kind == 'n')
       dma(Aoth, 8 + plan_index(kFwd ? kPlanFwd : kPlanDgrad, n, 'N'), t1);
     if constexpr (kind == 'A') {
-      constexpr int d = plan_index(kFwd ? kPlanFwd : kPlanDgrad, n, 'A');
-      // The wave's reads of Acur (sub-step 3's fragments) have returned.
-      if constexpr (d == 0) __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+      constexpr const char *plan = kFwd ? kPlanFwd : kPlanDgrad;
+      constexpr int d = plan_index(plan, n, 'A');
+      // The wave's reads of Acur (sub-step 3's fragments) have returned;
+      // weight-tile stores issued after them may still be pending.
+      if constexpr (d == 0)
+        __builtin_amdgcn_s_waitcnt(kWaitLgkm0 | (stores_after_reads(plan, n) << 8));
       dma(Acur, d, t2);
     }
-    if constexpr (kind == 'L') {
-      // One half-quarter of the product table.  Pinning the absmax here
-      // keeps the (pure) arithmetic at its slot.
-      constexpr int h = plan_index(kFwd ? kPlanFwd : kPlanDgrad, n, 'L');
-      float am = ta;
-      pin(am);
-      make_lut_half<false>(am, h, lutd, lut);
+    if constexpr (kind == 'M') {
+      // One quarter of the product table (two halves).
+      constexpr int h = 2 * plan_index(kFwd ? kPlanFwd : kPlanDgrad, n, 'M');
+      make_lut_half<false>(ta, h, lutd, lut);
+      make_lut_half<false>(ta, h + 1, lutd, lut);
     }
     if constexpr (kind == 'W') {
       constexpr int j = plan_index(kFwd ? kPlanFwd : kPlanDgrad, n, 'W');
       constexpr int k = j / kWordStages, stage = j % kWordStages;
-      // Each stage pins its inputs at its slot (see above).
       if constexpr (stage == 0) {
-        uint32_t w = prod.template word<kPhase>(k);
-        pin(w);
-        word_select_idx(w, wl);
+        word_select_idx(prod.template word<kPhase>(k), wl);
       } else if constexpr (stage == 1) {
-        uint32_t w = prod.template word<kPhase>(k);
-        pin(w);
-        word_select_mask(w, wl);
+        word_select_mask(prod.template word<kPhase>(k), wl);
       } else if constexpr (stage == 2) {
-        pin(wl.selE);
-        pin(wl.maskE);
         word_even(lut, wl);
       } else if constexpr (stage == 3) {
-        pin(wl.selO);
-        pin(wl.maskO);
         word_odd(lut, wl);
       } else if constexpr (stage == 4) {
-        pin(wl.loE);
-        pin(wl.hiE);
-        pin(wl.loO);
-        pin(wl.hiO);
         word_pairs(wl, wp[k]);
       } else {
         uint32_t o[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) pin(wp[k][e]);
         pairs_merge(wp[k], o);
         prod.template store<kPar, k, 0>(Bnext, o);
       }
