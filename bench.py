@@ -58,6 +58,10 @@ GEMM_SHAPES = {"70b_q": (8192, 8192, 8192), "70b_k": (8192, 1024, 8192),
                "7b_gate": (4096, 11008, 4096), "7b_down": (4096, 4096, 11008)}
 
 
+# Seconds of untimed warm-up before each timed workload (--warm-seconds).
+WARM_S = 0.5
+
+
 def algorithmic_bytes_dq(shapes, bs=64, group=256) -> int:
     total = 0
     for _, r, c in shapes:
@@ -72,6 +76,8 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--warm-seconds", type=float, default=WARM_S,
+                    help="untimed warm-up before each timed workload, after --warmup calls")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="approximate CPU time budget of the dequant cpu_baseline sample")
@@ -102,19 +108,33 @@ def make_weights(torch, nf4, shapes, seed):
     return ws
 
 
-def timed(torch, fn, steps, warmup):
+def timed(torch, fn, steps, warmup, warm_s=None, name=None):
     """Average ms of fn() over `steps` runs, HIP events on the current stream
-    (the stream every call here launches on)."""
+    (the stream every call here launches on).  Untimed warm-up: `warmup`
+    calls, then more calls until `warm_s` seconds have passed (WARM_S by
+    default): the GPU clock ramps up under load over a few tens of ms, and a
+    workload timed right after an idle phase (weight generation, another
+    config's setup) measured up to 15 % slow.  `name` labels the timed
+    launches with a marker range (roctx), which rocprofv3 --marker-trace
+    records, so a kernel trace can attribute them to their workload."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
+    deadline = time.perf_counter() + (WARM_S if warm_s is None else warm_s)
+    while time.perf_counter() < deadline:
+        fn()
+        torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
+    if name:
+        torch.cuda.nvtx.range_push(name)
     start.record()
     for _ in range(steps):
         fn()
     end.record()
     torch.cuda.synchronize()
+    if name:
+        torch.cuda.nvtx.range_pop()
     return start.elapsed_time(end) / steps
 
 
@@ -179,7 +199,8 @@ def bench_dequant(torch, nf4, args):
     ws = make_weights(torch, nf4, LAYER_7B, seed=2)
     outs = [torch.empty(w.shape, dtype=torch.bfloat16, device="cuda") for w in ws]
     log("timing the grouped dequant")
-    ms = timed(torch, lambda: nf4.dequant_batch(ws, outs), args.steps, args.warmup)
+    ms = timed(torch, lambda: nf4.dequant_batch(ws, outs), args.steps, args.warmup,
+               name="config2_dequant")
     return ws, ms
 
 
@@ -199,7 +220,7 @@ def bench_gemm(torch, nf4, gemm, args):
         gemm.linear_fwd_grouped(x, ws[:2], ys[:2])
         gemm.linear_fwd(xd, ws[2], ys[2])
     steps = max(3, args.steps // 5)
-    ms3 = timed(torch, cfg3, steps, 2)
+    ms3 = timed(torch, cfg3, steps, 2, name="config3")
     fl3 = sum(2.0 * 4096 * w.shape[0] * w.shape[1] for w in ws)
     tf3 = fl3 / (ms3 * 1e-3) / 1e12
     res["config3_7b_mlp_fwd"] = {"tflops": round(tf3, 1), "ms": round(ms3, 4), "flop": fl3,
@@ -242,15 +263,15 @@ def bench_gemm(torch, nf4, gemm, args):
         dgrad_pass()    # input gradient
 
     steps4 = max(2, args.steps // 10)
-    ms_f = timed(torch, fwd_pass, steps4, 1)
-    ms_d = timed(torch, dgrad_pass, steps4, 1)
-    ms_l = timed(torch, layer_step, steps4, 1)
+    ms_f = timed(torch, fwd_pass, steps4, 1, name="config4_fwd_pass")
+    ms_d = timed(torch, dgrad_pass, steps4, 1, name="config4_dgrad_pass")
+    ms_l = timed(torch, layer_step, steps4, 1, name="config4_layer_step")
     fl_pass = sum(2.0 * M * w.shape[0] * w.shape[1] for w in ws)
     per = {}
     for (name, _, _), a, w, y, dy, dx in zip(LAYER_70B, ins, ws, ys, dys, dxs):
         f = 2.0 * M * w.shape[0] * w.shape[1]
-        mf = timed(torch, lambda: gemm.linear_fwd(a, w, y), steps4, 1)
-        md = timed(torch, lambda: gemm.linear_dgrad(dy, w, dx), steps4, 1)
+        mf = timed(torch, lambda: gemm.linear_fwd(a, w, y), steps4, 1, name=f"fwd_{name}")
+        md = timed(torch, lambda: gemm.linear_dgrad(dy, w, dx), steps4, 1, name=f"dgrad_{name}")
         per[name] = {"fwd_tflops": round(f / (mf * 1e-3) / 1e12, 1),
                      "dgrad_tflops": round(f / (md * 1e-3) / 1e12, 1)}
     # The first forward of a double-pass step only hands `hidden` to down:
@@ -263,10 +284,12 @@ def bench_gemm(torch, nf4, gemm, args):
         gemm.linear_swiglu(h, ws[4], ws[5], hsw)
         gemm.linear_fwd(hsw, ws[6], ys[6])
 
-    ms_fs = timed(torch, fwd_pass_swiglu, steps4, 1)
+    ms_fs = timed(torch, fwd_pass_swiglu, steps4, 1, name="config4_fwd_pass_swiglu")
     fl_gu = 2 * 2.0 * M * 28672 * 8192
-    ms_gu = timed(torch, lambda: gemm.linear_fwd_grouped(h, ws[4:6], ys[4:6]), steps4, 1)
-    ms_sw = timed(torch, lambda: gemm.linear_swiglu(h, ws[4], ws[5], hsw), steps4, 1)
+    ms_gu = timed(torch, lambda: gemm.linear_fwd_grouped(h, ws[4:6], ys[4:6]), steps4, 1,
+                  name="gate_up_grouped")
+    ms_sw = timed(torch, lambda: gemm.linear_swiglu(h, ws[4], ws[5], hsw), steps4, 1,
+                  name="gate_up_swiglu")
     tf_l = 3 * fl_pass / (ms_l * 1e-3) / 1e12
     res["config4_70b_layer"] = {
         "tflops": round(tf_l, 1), "ms_per_layer_step": round(ms_l, 3),
@@ -378,7 +401,7 @@ def bench_one_gemm(torch, nf4, gemm, args):
         a = torch.randn(m, n, device="cuda", generator=g).to(torch.bfloat16)
         o = torch.empty(m, k, dtype=torch.bfloat16, device="cuda")
         fn = lambda: gemm.linear_dgrad(a, w, o)
-    ms = timed(torch, fn, args.steps, args.warmup)
+    ms = timed(torch, fn, args.steps, args.warmup, name=f"{args.gemm_shape}_{args.gemm_mode}")
     tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
     print(json.dumps({"gemm_shape": args.gemm_shape, "mode": args.gemm_mode, "m": m, "n": n,
                       "k": k, "ms": round(ms, 4), "tflops": round(tf, 1)}), flush=True)
@@ -393,7 +416,7 @@ def bf16_gemm_reference(torch, dequant_gbs, layer_ms):
     a = torch.randn(m, k, device="cuda", generator=g).to(torch.bfloat16)
     b = torch.randn(n, k, device="cuda", generator=g).to(torch.bfloat16)
     o = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
-    ms = timed(torch, lambda: torch.matmul(a, b.t(), out=o), 5, 2)
+    ms = timed(torch, lambda: torch.matmul(a, b.t(), out=o), 5, 2, name="bf16_reference")
     tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
     res = {"op": "torch.matmul bf16 (hipBLASLt), M=8192 N=28672 K=8192", "tflops": round(tf, 1),
            "frac_of_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4)}
@@ -420,7 +443,9 @@ def copy_calibration(torch):
 
 
 def main():
+    global WARM_S
     args = parse()
+    WARM_S = args.warm_seconds
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU (every GPU box here has one); "
                                    "bench.py --gpus N with N > 1 is not supported"}))
@@ -440,7 +465,8 @@ def main():
     line = {
         "metric": "NF4 dequant HBM GB/s (% peak); NF4-fused GEMM TFLOP/s at 7B/70B layer shapes",
         "value": None, "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": None, "higher_is_better": True,
+        "warmup": args.warmup, "warm_seconds": args.warm_seconds, "ms_per_step": None,
+        "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic: torch.randn weights (sigma 0.02) quantized on device, "
                 "randn activations",
