@@ -1,0 +1,335 @@
+// bf16_wgrad.hip - weight gradient dW = dY^T . X for gfx950 (MI355X).
+//
+//   dw[n, k] (+)= sum_m dy[m, n] * x[m, k]
+// the d_wd / d_wg / d_wu / d_wo / d_wq / d_wk / d_wv loops of
+// single_layer_backward (doublepass/src/backward.rs:87-93, 117-129, 160-168,
+// 284-300), with the micro-batch accumulation of backward.rs:478-502 as the
+// `accumulate` flag.  dy [M, N] and x [M, K] are bf16, row-major; dw [N, K]
+// fp32.  The reduction runs over the token index m, the row index of both
+// operands, so both MFMA operands are columns of row-major tiles.
+//
+// Workgroup = 4 waves in 2 x 2, tile = 256 dW rows (n) x 256 dW columns (k);
+// each wave owns 128 x 128 in 256 accumulator registers (16 tiles of
+// v_mfma_f32_32x32x16_bf16).  Per 64-token step the dy tile (64 x 256 bf16)
+// and the x tile (64 x 256) move into LDS with direct-to-LDS loads (two
+// stages of 64 KB), and each wave reads its fragments with the transposing
+// ds_read_b64_tr_b16: 8 consecutive tokens of one column per lane.
+#include "abi_common.hpp"
+#include "gemm_common.hpp"
+#include "nf4_device.hpp"
+
+namespace nf4s {
+
+constexpr int kWgThreads = 256;
+constexpr int kWgTile = 256;  // dW rows and columns per workgroup
+constexpr int kWgStep = 64;   // tokens per step
+
+struct WgradArgs {
+  const uint16_t *dy;  // [M, N], row stride N
+  const uint16_t *x;   // [M, K], row stride K
+  float *dw;           // [N, K], row stride K
+  int64_t M, N, K;
+  int32_t tiles_n, tiles_k;
+  int32_t accumulate;
+};
+
+// LDS tile: 64 token rows x 256 columns (512 B = 32 units of 16 B per row).
+// A wave reads one 128-column half (16 units).  Unit u of row r lives at
+// physical unit (u & 16) | ((u & 15) ^ 5 (r % 4)): with it, each 32-lane
+// half of a transposed fragment read covers 16 distinct 16-B units of one
+// half-row's 64 banks (rows are 512 B = 128 banks apart, so every row starts
+// at bank 0), and each 16-lane quarter of a DMA writes one row's 16
+// contiguous units.
+__device__ __forceinline__ int wg_unit(int row, int u) {
+  return (u & 16) | ((u & 15) ^ (5 * (row & 3)));
+}
+
+// [stage][operand 0 = dy, 1 = x][row * 32 + unit]: 2 x 2 x 32 KB.
+__shared__ u32x4 g_wg_lds[2][2][64 * 32];
+
+// Byte offset (from its tile's base) of lane `lane`'s first transposed read
+// of fragment j: column 32j + lane % 32 of the wave's half h, token rows
+// 8 (lane / 32) + 0..3 of sub-step 0.  ds_read_b64_tr_b16 transposes 4 x 4
+// blocks of 16-bit values within each 16-lane group: lane i receives element
+// i % 4 of the 8 bytes that lane 4e + i / 4 addresses, so lane 4e + c
+// addresses row e, columns 4c..4c+3 of the group's 16-column strip.  A second
+// read 4 rows lower completes the 8 tokens.
+__device__ __forceinline__ uint32_t wg_read_off(int lane, int h, int j) {
+  const int l16 = lane & 15, e = l16 >> 2;
+  const int row = 8 * (lane >> 5) + e;
+  const int u = 16 * h + 4 * j + 2 * ((lane >> 4) & 1) + ((l16 >> 1) & 1);
+  return (uint32_t)(512 * row + 16 * wg_unit(row, u) + 8 * (l16 & 1));
+}
+
+// Fragment (8 tokens of one column, sub-step s) from the tile at `base`.
+__device__ __forceinline__ u32x4 wg_frag(const char *base, uint32_t off, int s) {
+  typedef __attribute__((address_space(3))) char lds_char_t;
+  typedef __attribute__((address_space(3))) v4i16 lds_v4i16_t;
+  lds_char_t *p = (lds_char_t *)const_cast<char *>(base) + off + 8192 * s;
+  const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t *)p);
+  const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t *)(p + 2048));
+  const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+  return (u32x4){l2.x, l2.y, h2.x, h2.y};
+}
+
+// Fragment read q (0..7) of a sub-step in the order the sub-step's first
+// MFMAs use them: dy0, x0, x1, x2, x3, dy1, dy2, dy3.
+__device__ __forceinline__ void wg_read(const char *tdy, const char *tx, const uint32_t (&rdy)[4],
+                                        const uint32_t (&rx)[4], u32x4 (&fd)[4], u32x4 (&fx)[4],
+                                        int s, int q) {
+  if (q == 0 || q >= 5) {
+    const int j = (q == 0) ? 0 : q - 4;
+    fd[j] = wg_frag(tdy, rdy[j], s);
+  } else {
+    fx[q - 1] = wg_frag(tx, rx[q - 1], s);
+  }
+}
+
+// One 64-token step t from stage `cur`: 4 sub-steps of 16 MFMAs; the
+// fragments of sub-step s+1 are read (one per MFMA slot) during sub-step s,
+// and step t+1's 16 DMAs of this wave (8 dy rows, 8 x rows, two 256-column
+// rows per instruction) go into the other stage during sub-steps 0-1.  That
+// stage was last read in step t-1, before the barrier that ended it.  The
+// barrier after MFMA 7 of sub-step 3 waits for every DMA and LDS read; the
+// last 8 MFMAs (operands in registers) open the next call, each followed by
+// one of the next step's sub-step 0 reads.
+// The four LDS tiles come in as distinct __restrict__ pointers: the
+// compiler then knows that DMAs into the next stage never alias the reads of
+// the current one and waits (vmcnt) only at the barrier.
+__device__ __forceinline__ void wgrad_step(floatx16 (&acc)[4][4], u32x4 (&fd)[2][4],
+                                           u32x4 (&fx)[2][4], const char *__restrict__ cur_dy,
+                                           const char *__restrict__ cur_x,
+                                           char *__restrict__ nxt_dy, char *__restrict__ nxt_x,
+                                           const uint32_t (&rdy)[4], const uint32_t (&rx)[4],
+                                           __amdgpu_buffer_rsrc_t rs_dy, __amdgpu_buffer_rsrc_t rs_x,
+                                           uint32_t (&vdy)[8], uint32_t (&vx)[8],
+                                           uint32_t step_dy, uint32_t step_x, bool more, int wave) {
+  // Previous step's last 8 MFMAs, then this step's sub-step 0 reads.
+  static_for<0, 8>([&](auto I) {
+    constexpr int i = decltype(I)::value;
+    constexpr int mt = 2 + (i >> 2), nt = i & 3;
+    acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+        __builtin_bit_cast(bf16x8, fx[1][nt]), __builtin_bit_cast(bf16x8, fd[1][mt]),
+        acc[mt][nt], 0, 0, 0);
+    wg_read(cur_dy, cur_x, rdy, rx, fd[0], fx[0], 0, i);
+    __builtin_amdgcn_sched_barrier(0);
+  });
+  static_for<0, 56>([&](auto N) {
+    constexpr int n = decltype(N)::value;
+    constexpr int s = n / 16, i = n % 16;
+    constexpr int mt = i >> 2, nt = i & 3;
+    acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+        __builtin_bit_cast(bf16x8, fx[s & 1][nt]), __builtin_bit_cast(bf16x8, fd[s & 1][mt]),
+        acc[mt][nt], 0, 0, 0);
+    if constexpr (s < 3 && i < 8)
+      wg_read(cur_dy, cur_x, rdy, rx, fd[(s + 1) & 1], fx[(s + 1) & 1], s + 1, i);
+    if constexpr (s < 2 && (i & 1) == 1) {
+      // DMA d = 8 s + i / 2: operand d / 8, instruction d % 8 (rows 16 wave +
+      // 2 (d % 8) and the next).
+      constexpr int d = 8 * s + i / 2;
+      if (more) {
+        if constexpr (d < 8) {
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(
+              rs_dy, (lds_void_t *)(nxt_dy + 1024 * (8 * wave + d)), 16,
+              (int)vdy[d], 0, 0, 0);
+          vdy[d] += step_dy;
+        } else {
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(
+              rs_x, (lds_void_t *)(nxt_x + 1024 * (8 * wave + d - 8)), 16, (int)vx[d - 8], 0, 0,
+              0);
+          vx[d - 8] += step_x;
+        }
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  });
+  step_barrier<0>();
+}
+
+// One output tile: its 256 x 256 dW block over all M tokens.
+__global__ void __launch_bounds__(kWgThreads, 1) wgrad_kernel(const WgradArgs g) {
+  const int T = g.tiles_n * g.tiles_k;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int hn = wave >> 1, hk = wave & 1;  // the wave's halves of n and k
+  uint32_t rdy[4], rx[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    rdy[j] = wg_read_off(lane, hn, j);
+    rx[j] = wg_read_off(lane, hk, j);
+  }
+  char *lds0_dy = reinterpret_cast<char *>(&g_wg_lds[0][0][0]);
+  char *lds0_x = reinterpret_cast<char *>(&g_wg_lds[0][1][0]);
+  char *lds1_dy = reinterpret_cast<char *>(&g_wg_lds[1][0][0]);
+  char *lds1_x = reinterpret_cast<char *>(&g_wg_lds[1][1][0]);
+  const int64_t nsteps = (g.M + kWgStep - 1) / kWgStep;
+  const uint32_t step_dy = (uint32_t)(kWgStep * g.N * 2);
+  const uint32_t step_x = (uint32_t)(kWgStep * g.K * 2);
+#pragma unroll 1
+  for (int b = blockIdx.x; b < T; b += gridDim.x) {
+    int tn, tk;
+    map_tile(b, g.tiles_n, g.tiles_k, tn, tk);
+    const int64_t n0 = (int64_t)tn * kWgTile, k0 = (int64_t)tk * kWgTile;
+    // Buffer resources based at the tiles' first columns; num_records ends
+    // at the matrix end, so token rows >= M (and the last row's columns past
+    // the end) read as zero.  Columns past N or K of other rows read the next
+    // row's values and only reach outputs that are never stored.
+    const __amdgpu_buffer_rsrc_t rs_dy = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(g.dy + n0), 0, (int)(g.M * g.N * 2 - n0 * 2), kBufferFlags);
+    const __amdgpu_buffer_rsrc_t rs_x = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(g.x + k0), 0, (int)(g.M * g.K * 2 - k0 * 2), kBufferFlags);
+    // Lane offsets of this wave's 8 DMAs per operand for step 0: instruction
+    // d writes rows 16 wave + 2d + (lane / 32), physical unit lane % 32.
+    uint32_t vdy[8], vx[8];
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+      const int r = 16 * wave + 2 * d + (lane >> 5);
+      const int u = wg_unit(r, lane & 31);  // the logical unit stored at physical lane % 32
+      vdy[d] = (uint32_t)(r * g.N * 2 + 16 * u);
+      vx[d] = (uint32_t)(r * g.K * 2 + 16 * u);
+    }
+    // Prologue: step 0's tiles into stage 0.
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_dy, (lds_void_t *)(lds0_dy + 1024 * (8 * wave + d)),
+                                               16, (int)vdy[d], 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_x, (lds_void_t *)(lds0_x + 1024 * (8 * wave + d)),
+                                               16, (int)vx[d], 0, 0, 0);
+      vdy[d] += step_dy;
+      vx[d] += step_x;
+    }
+    step_barrier<0>();
+
+    floatx16 acc[4][4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[mt][nt][v] = 0.0f;
+    u32x4 fd[2][4], fx[2][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      fd[1][i] = (u32x4){0u, 0u, 0u, 0u};
+      fx[1][i] = (u32x4){0u, 0u, 0u, 0u};
+    }
+    int64_t t = 0;
+#pragma unroll 1
+    for (; t + 2 <= nsteps; t += 2) {
+      wgrad_step(acc, fd, fx, lds0_dy, lds0_x, lds1_dy, lds1_x, rdy, rx, rs_dy, rs_x, vdy, vx,
+                 step_dy, step_x, t + 1 < nsteps, wave);
+      wgrad_step(acc, fd, fx, lds1_dy, lds1_x, lds0_dy, lds0_x, rdy, rx, rs_dy, rs_x, vdy, vx,
+                 step_dy, step_x, t + 2 < nsteps, wave);
+    }
+    if (t < nsteps)
+      wgrad_step(acc, fd, fx, lds0_dy, lds0_x, lds1_dy, lds1_x, rdy, rx, rs_dy, rs_x, vdy, vx,
+                 step_dy, step_x, false, wave);
+    // The last step's final 8 MFMAs.
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int mt = 2 + (i >> 2), nt = i & 3;
+      acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+          __builtin_bit_cast(bf16x8, fx[1][nt]), __builtin_bit_cast(bf16x8, fd[1][mt]),
+          acc[mt][nt], 0, 0, 0);
+    }
+
+    // Epilogue.  Lane l holds dW row n = n0 + 128 hn + 32 mt + l % 32 and
+    // columns k = k0 + 128 hk + 32 nt + 8 j + 4 (l / 32) + i in registers
+    // 4 j + i of tile [mt][nt]: four adjacent fp32 per 16-B store.
+    const int jl = lane & 31, grp = lane >> 5;
+    const bool vec_ok = ((reinterpret_cast<uintptr_t>(g.dw) & 15) == 0) && ((g.K & 3) == 0);
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      const int64_t n = n0 + 128 * hn + 32 * mt + jl;
+      if (n < g.N) {
+        float *row = g.dw + n * g.K;
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int64_t k = k0 + 128 * hk + 32 * nt + 8 * j + 4 * grp;
+            floatx4 v = {acc[mt][nt][4 * j], acc[mt][nt][4 * j + 1], acc[mt][nt][4 * j + 2],
+                         acc[mt][nt][4 * j + 3]};
+            if (vec_ok && k + 4 <= g.K) {
+              floatx4 *p = reinterpret_cast<floatx4 *>(row + k);
+              if (g.accumulate) v += *p;
+              *p = v;
+            } else {
+#pragma unroll
+              for (int i = 0; i < 4; ++i)
+                if (k + i < g.K) row[k + i] = g.accumulate ? row[k + i] + v[i] : v[i];
+            }
+          }
+      }
+    }
+    // The next tile's prologue DMAs overwrite stage 0, which the last
+    // step's reads may have used: every wave's reads end before this.
+    step_barrier<0>();
+  }
+}
+
+__global__ void fill_zero_f32(float *__restrict__ p, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = 0.0f;
+}
+
+static int32_t wgrad(const uint16_t *dy, const uint16_t *x, int64_t m, int64_t n, int64_t k,
+                     float *dw, int32_t accumulate, hipStream_t s) {
+  if (dw == nullptr) return fail(NF4S_ERR_INVALID_ARGUMENT, "dw is NULL");
+  if (m > 0 && (dy == nullptr || x == nullptr))
+    return fail(NF4S_ERR_INVALID_ARGUMENT, "dy or x is NULL");
+  if (m < 0 || n <= 0 || k <= 0)
+    return fail(NF4S_ERR_INVALID_ARGUMENT, "bad weight-gradient shape m=%lld n=%lld k=%lld",
+                (long long)m, (long long)n, (long long)k);
+  if (n % 8 != 0 || k % 8 != 0)
+    return fail(NF4S_ERR_UNSUPPORTED_SHAPE, "weight gradient needs n %% 8 == 0 and k %% 8 == 0, "
+                "got n=%lld k=%lld", (long long)n, (long long)k);
+  if (!aligned(dy, 16) || !aligned(x, 16))
+    return fail(NF4S_ERR_MISALIGNED, "dy and x must be 16-byte aligned");
+  if (!aligned(dw, 4)) return fail(NF4S_ERR_MISALIGNED, "dw must be 4-byte aligned");
+  // Lane offsets are 32-bit and a step's offset must stay below 2^31.
+  const int64_t lim = ((int64_t)1 << 31) - 1;
+  if (m * n * 2 > lim || m * k * 2 > lim)
+    return fail(NF4S_ERR_UNSUPPORTED_SHAPE, "dy or x larger than 2 GiB (m=%lld n=%lld k=%lld)",
+                (long long)m, (long long)n, (long long)k);
+  WgradArgs g{};
+  g.dy = dy;
+  g.x = x;
+  g.dw = dw;
+  g.M = m;
+  g.N = n;
+  g.K = k;
+  g.tiles_n = (int32_t)((n + kWgTile - 1) / kWgTile);
+  g.tiles_k = (int32_t)((k + kWgTile - 1) / kWgTile);
+  g.accumulate = accumulate ? 1 : 0;
+  const int64_t T = (int64_t)g.tiles_n * g.tiles_k;
+  if (T > 0x7fffffff) return fail(NF4S_ERR_UNSUPPORTED_SHAPE, "too many tiles");
+  if (m == 0) {
+    // An empty sum: dw += 0, or dw = 0 (a fill kernel rather than
+    // hipMemsetAsync, so that a caller may capture the call in a HIP graph).
+    // The main kernel's buffer bounds assume m > 0.
+    if (accumulate) return NF4S_OK;
+    const int64_t cnt = n * k;
+    const int64_t blocks = (cnt + 255) / 256;
+    hipLaunchKernelGGL(fill_zero_f32, dim3((uint32_t)(blocks < 65536 ? blocks : 65536)), dim3(256),
+                       0, s, dw, cnt);
+    return check_launch("fill_zero_f32");
+  }
+  hipLaunchKernelGGL(wgrad_kernel, dim3(persistent_grid(T)), dim3(kWgThreads), 0, s, g);
+  return check_launch("wgrad_kernel");
+}
+
+}  // namespace nf4s
+
+using namespace nf4s;
+
+extern "C" {
+
+int32_t nf4s_gemm_wgrad(const void *dy, const void *x, int64_t m, int64_t n, int64_t k,
+                        float *dw, int32_t accumulate, void *stream) {
+  return wgrad(static_cast<const uint16_t *>(dy), static_cast<const uint16_t *>(x), m, n, k, dw,
+               accumulate, as_stream(stream));
+}
+
+}  // extern "C"

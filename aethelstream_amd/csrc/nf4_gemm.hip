@@ -26,36 +26,18 @@
 // accumulator layout is lane l: column l % 32, row 8(v/4) + 4g + v%4; the
 // weight fragment is the first operand, so the accumulator's columns are
 // activation rows and its rows are output columns.
-#include <atomic>
 #include <type_traits>
 
 #include "abi_common.hpp"
+#include "gemm_common.hpp"
 #include "nf4_device.hpp"
 
 namespace nf4s {
-
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef short v4i16 __attribute__((ext_vector_type(4)));
-typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr int kGemmThreads = 256;
 constexpr int kTileM = 512;   // activation rows per workgroup (128 per wave)
 constexpr int kTileO = 128;   // output columns per workgroup
 constexpr int kStep = 64;     // reduction depth per step (= NF4 block size)
-
-// Compile-time loop: f(IC<B>{}), ..., f(IC<E-1>{}).  Slot plans, fragment
-// indices and LDS immediate offsets are then constant expressions.
-template <int N>
-struct IC {
-  static constexpr int value = N;
-};
-template <int B, int E, class F>
-__device__ __forceinline__ void static_for(F &&f) {
-  if constexpr (B < E) {
-    f(IC<B>{});
-    static_for<B + 1, E>(f);
-  }
-}
 
 struct GemmArgs {
   const uint16_t *a;  // activation [M, R] row-major (x or dy)
@@ -450,20 +432,6 @@ struct DgradProducer : PerStepLoads<kDQ, DgradProducer<kDQ>> {
   }
 };
 
-// Maps tile index b to (tile_m, tile_o).  Workgroups are dispatched
-// round-robin over the 8 XCDs and the persistent grid is a multiple of 8, so
-// tile b runs on XCD b % 8; consecutive logical tiles (same activation rows,
-// neighbouring output columns) are given to the same XCD so that its
-// resident workgroups share the activation rows in that XCD's L2.
-__device__ __forceinline__ void map_tile(int b, int tiles_m, int tiles_o, int &tm, int &to) {
-  const int T = tiles_m * tiles_o;
-  const int x = b & 7, qq = b >> 3;
-  const int base = T >> 3, rem = T & 7;
-  const int L = x * base + (x < rem ? x : rem) + qq;
-  tm = L / tiles_o;
-  to = L - tm * tiles_o;
-}
-
 // LDS: two activation buffers per wave (128 rows x 128 B = 16 KB each, a
 // wave's pair adjacent) and two weight tiles (16 KB each): 160 KB, the gfx950
 // maximum.  With the buffers of a pair 16 KB apart, the main loop (unrolled
@@ -471,34 +439,6 @@ __device__ __forceinline__ void map_tile(int b, int tiles_m, int tiles_o, int &t
 // offsets from loop-invariant lane addresses.
 __shared__ u32x4 g_lds_a[4][2][1024];
 __shared__ u32x4 g_lds_b[2][1024];
-
-typedef __attribute__((address_space(3))) void lds_void_t;
-
-// Word 3 of a raw (stride 0) gfx9 buffer resource: 32-bit data format.
-constexpr int kBufferFlags = 0x00020000;
-
-// s_waitcnt immediates (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] |
-// lgkmcnt[11:8] | vmcnt[5:4] << 14).
-constexpr int kWaitLgkm0 = 0xC07F;       // lgkmcnt(0), vmcnt and expcnt not waited
-// vmcnt(n) lgkmcnt(0), expcnt not waited.
-constexpr int wait_vm_lgkm0(int n) { return (n & 15) | 0x70 | ((n >> 4) << 14); }
-
-// Workgroup barrier without the memory-model fences of __syncthreads(): the
-// release fence would wait for every outstanding load (vmcnt(0)), including
-// the activation DMAs that are meant to stay in flight across it.  The waits
-// the barrier needs are issued explicitly before it (all but the kInFlight
-// most recent vector-memory operations, and every LDS operation); the empty asm
-// keeps the compiler from moving memory operations across it.
-template <int kInFlight>
-__device__ __forceinline__ void step_barrier() {
-  __builtin_amdgcn_sched_barrier(0);
-  __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(kInFlight));
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_sched_barrier(0);
-}
-
 
 // Fragment read k (0..7) of sub-step s into register buffer n, in the order
 // the sub-step's first MFMAs consume them: A0, B0, B1, B2, B3, A1, A2, A3.
@@ -1168,28 +1108,6 @@ static GemmGroup group_of(const nf4s_tensor &w, int64_t wn) {
   q.am = absmax_of(w);
   q.wn = wn;
   return q;
-}
-
-// Persistent grid: one workgroup per compute unit (a workgroup takes all of
-// a CU's LDS), each looping over tiles b, b + grid, ...  A tile's output
-// stores then drain while the same workgroup's next tile starts loading,
-// instead of every CU storing and then loading in lockstep at each round of
-// tiles.  The CU count is read once per device; a multiple of 8 keeps tile
-// b on XCD b % 8 (map_tile).
-static uint32_t persistent_grid(int64_t tiles) {
-  static std::atomic<int> cus[64];  // zero-initialized (static storage)
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-  int c = cus[dev].load(std::memory_order_relaxed);
-  if (c == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        n <= 0)
-      n = 256;
-    c = (n + 7) & ~7;
-    cus[dev].store(c, std::memory_order_relaxed);  // every caller stores the same value
-  }
-  return (uint32_t)(tiles < c ? tiles : c);
 }
 
 template <class Producer>

@@ -12,6 +12,8 @@
                  forward.rs:251-254 fused into the GEMM epilogue.
 ``linear_dgrad_sum``    dx = sum_i dy_i . W_i, one launch and one rounding
                  (d_h1 at backward.rs:284-300, d_h2 at backward.rs:117-129).
+``linear_wgrad``        dW = dy^T . x in fp32, the weight gradients beside them
+                 (backward.rs:87-93, 117-129, 160-168, 284-300).
 
 x / dy are bf16 [M, K] / [M, N] device tensors, W an :class:`Nf4Weight` of
 shape [N, K]; accumulation is fp32 in MFMA, the output bf16.
@@ -136,6 +138,31 @@ def linear_dgrad_sum(dys: Sequence[torch.Tensor], ws: Sequence[Nf4Weight],
     descs = _descs(ws)
     _lib.check(_lib.load().nf4s_gemm_dgrad_sum(dps, descs, ns, len(ws), m, k, out.data_ptr(),
                                                _stream_ptr(out)))
+    return out
+
+
+def linear_wgrad(dy: torch.Tensor, x: torch.Tensor, out: Optional[torch.Tensor] = None,
+                 accumulate: bool = False) -> torch.Tensor:
+    """dW[N, K] = dy[M, N]^T . x[M, K] in fp32 (bf16 inputs), or dW += that sum
+    when ``accumulate`` (the micro-batch sum of backward.rs:478-502).  The
+    weight gradients of single_layer_backward (backward.rs:87-93, 117-129,
+    160-168, 284-300); no NF4 operand."""
+    _require_cuda(dy, x)
+    if dy.dtype != torch.bfloat16 or x.dtype != torch.bfloat16:
+        raise ValueError("dy and x must be bfloat16")
+    if dy.dim() != 2 or x.dim() != 2 or dy.shape[0] != x.shape[0]:
+        raise ValueError(f"dy [M, N] and x [M, K] must share M, got {list(dy.shape)} and "
+                         f"{list(x.shape)}")
+    m, n, k = dy.shape[0], dy.shape[1], x.shape[1]
+    if out is None:
+        if accumulate:
+            raise ValueError("accumulate needs an existing out tensor")
+        out = torch.empty(n, k, dtype=torch.float32, device=dy.device)
+    _require_cuda(out)
+    if out.dtype != torch.float32 or list(out.shape) != [n, k]:
+        raise ValueError(f"out must be float32 [{n}, {k}]")
+    _lib.check(_lib.load().nf4s_gemm_wgrad(dy.data_ptr(), x.data_ptr(), m, n, k, out.data_ptr(),
+                                           1 if accumulate else 0, _stream_ptr(dy)))
     return out
 
 

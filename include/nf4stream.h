@@ -200,6 +200,19 @@ int32_t nf4s_gemm_dgrad_sum(const uint16_t *const *dys, const nf4s_tensor *ws,
                             const int64_t *ns, int32_t count, int64_t m,
                             int64_t k, uint16_t *dx, void *stream);
 
+/*
+ * Weight gradient, bf16 in, fp32 out: dw[n, k] = sum_m dy[m, n] * x[m, k]
+ * (accumulate = 0), or dw += that sum (accumulate != 0).  Replaces the d_wd,
+ * d_wg / d_wu, d_wo and d_wq / d_wk / d_wv loops of single_layer_backward
+ * (doublepass/src/backward.rs:87-93, 117-129, 160-168, 284-300); accumulate
+ * is the micro-batch sum of backward.rs:478-502.  dy [m, n] and x [m, k] are
+ * row-major bf16 with n % 8 == 0 and k % 8 == 0, 16-byte aligned; dw [n, k]
+ * row-major fp32.  dy and x must each be below 2 GiB.  No NF4 operand: this
+ * is the plain bf16 GEMM the backward pass needs beside the fused ones.
+ */
+int32_t nf4s_gemm_wgrad(const void *dy, const void *x, int64_t m, int64_t n,
+                        int64_t k, float *dw, int32_t accumulate, void *stream);
+
 /* ---------------------------------------------------------------------------
  * Streamed layer stack (one GPU).  Layers wait in pinned host memory and are
  * copied into a two-slot device double buffer on a dedicated copy stream.

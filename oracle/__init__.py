@@ -56,6 +56,7 @@ def lib():
             f.restype = ctypes.c_int
         L.or_matmul_tb.argtypes = [P, P, i64, i64, i64, P]
         L.or_dgrad.argtypes = [P, P, i64, i64, i64, P]
+        L.or_wgrad.argtypes = [P, P, i64, i64, i64, P]
         L.or_gen_normal.argtypes = [ctypes.c_uint64, i64, ctypes.c_double, P]
         _lib = L
     return _lib
@@ -151,6 +152,17 @@ def dgrad(dy: np.ndarray, w: np.ndarray) -> np.ndarray:
     dx = np.zeros((m, k), np.float32)
     lib().or_dgrad(_p(dy), _p(w), m, n, k, _p(dx))
     return dx
+
+
+def wgrad(dy: np.ndarray, x: np.ndarray, dw: np.ndarray = None) -> np.ndarray:
+    """backward.rs:87-93: dw[n,k] (+)= sum_m dy[m,n] x[m,k] in fp32."""
+    dy = np.ascontiguousarray(dy, np.float32)
+    x = np.ascontiguousarray(x, np.float32)
+    m, n = dy.shape
+    k = x.shape[1]
+    out = np.zeros((n, k), np.float32) if dw is None else np.array(dw, np.float32, copy=True)
+    lib().or_wgrad(_p(dy), _p(x), m, n, k, _p(out))
+    return out
 
 
 def bf16_bits_to_f32(bits: np.ndarray) -> np.ndarray:

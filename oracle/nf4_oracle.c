@@ -245,6 +245,16 @@ void or_matmul_tb(const float *a, const float *b, int64_t m, int64_t k,
         }
 }
 
+/* doublepass/src/backward.rs:87-93 (d_wd[k*ff+j] += d_mlp_out[i*d+k] *
+ * hidden[i*ff+j], outer loops over the gradient's element, inner over the
+ * tokens i). */
+void or_wgrad(const float *dy, const float *x, int64_t m, int64_t n,
+              int64_t k, float *dw) {
+    for (int64_t r = 0; r < n; ++r)
+        for (int64_t c = 0; c < k; ++c)
+            for (int64_t i = 0; i < m; ++i) dw[r * k + c] += dy[i * n + r] * x[i * k + c];
+}
+
 /* doublepass/src/backward.rs:160-168 (d_attn_out += d_out_proj . Wo); the
  * sites :79-85, :117-129 and :284-300 have the same shape. */
 void or_dgrad(const float *dy, const float *w, int64_t m, int64_t n,

@@ -24,6 +24,8 @@
  *                        (q in [0,127], group max -> 127, |a'-a| <= s2/2)
  *   or_matmul_tb         closed form vs fp64 numpy on small shapes
  *   or_dgrad             closed form vs fp64 numpy on small shapes
+ *   or_wgrad             closed form vs fp64 numpy on small shapes; exact on
+ *                        small-integer data
  */
 #ifndef NF4_ORACLE_H
 #define NF4_ORACLE_H
@@ -95,6 +97,13 @@ void or_matmul_tb(const float *a, const float *b, int64_t m, int64_t k,
  * dx must be zeroed by the caller for a fresh result. */
 void or_dgrad(const float *dy, const float *w, int64_t m, int64_t n,
               int64_t k, float *dx);
+
+/* Weight-gradient loop (doublepass/src/backward.rs:87-93, d_wd):
+ * dw[n,k] += dy[m,n] . x[m,k] summed over m, fp32, for n, for k, for m
+ * order; the sites :117-129, :160-168 and :284-300 have the same form.
+ * dw must be zeroed by the caller for a fresh result. */
+void or_wgrad(const float *dy, const float *x, int64_t m, int64_t n,
+              int64_t k, float *dw);
 
 /* Deterministic input generator: splitmix64(seed) -> 53-bit uniform ->
  * Box-Muller in fp64 -> * sigma -> fp32 round to nearest. */

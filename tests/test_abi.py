@@ -70,6 +70,21 @@ def test_invalid_arguments():
     assert lib.nf4s_dq_encode(0x1000, 10, 0, 0x1000, 0x1000, None) == _lib.NF4S_ERR_INVALID_ARGUMENT
 
 
+def test_wgrad_argument_rejection():
+    """nf4s_gemm_wgrad validates before touching the device."""
+    lib = _lib.load()
+    f = lib.nf4s_gemm_wgrad
+    assert f(None, 0x1000, 64, 64, 64, 0x1000, 0, None) == _lib.NF4S_ERR_INVALID_ARGUMENT
+    assert f(0x1000, 0x1000, 64, 64, 64, None, 0, None) == _lib.NF4S_ERR_INVALID_ARGUMENT
+    assert f(0x1000, 0x1000, 64, 0, 64, 0x1000, 0, None) == _lib.NF4S_ERR_INVALID_ARGUMENT
+    assert f(0x1000, 0x1000, -1, 64, 64, 0x1000, 0, None) == _lib.NF4S_ERR_INVALID_ARGUMENT
+    assert f(0x1000, 0x1000, 64, 12, 64, 0x1000, 0, None) == _lib.NF4S_ERR_UNSUPPORTED_SHAPE
+    assert f(0x1000, 0x1000, 64, 64, 20, 0x1000, 0, None) == _lib.NF4S_ERR_UNSUPPORTED_SHAPE
+    assert f(0x1008, 0x1000, 64, 64, 64, 0x1000, 0, None) == _lib.NF4S_ERR_MISALIGNED
+    assert f(0x1000, 0x1000, 64, 64, 64, 0x1002, 0, None) == _lib.NF4S_ERR_MISALIGNED
+    assert f(0x1000, 0x1000, 1 << 20, 1024, 64, 0x1000, 0, None) == _lib.NF4S_ERR_UNSUPPORTED_SHAPE
+
+
 def test_python_mirror_raises_malformed_index():
     import torch
     from aethelstream_amd import nf4

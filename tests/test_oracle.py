@@ -183,6 +183,25 @@ def test_matmul_tb_and_dgrad_against_fp64():
     np.testing.assert_allclose(acc, dx + 1, rtol=1e-5, atol=1e-5)
 
 
+def test_wgrad_against_fp64_and_exact_integers():
+    """or_wgrad (backward.rs:87-93) is dy^T . x: fp64 closed form on a
+    non-square shape (a transposed or swapped operand changes the shape or the
+    values), exact on small integers, and += into the caller's buffer."""
+    rng = np.random.default_rng(5)
+    dy = rng.standard_normal((29, 12)).astype(np.float32)
+    x = rng.standard_normal((29, 20)).astype(np.float32)
+    dw = oracle.wgrad(dy, x)
+    assert dw.shape == (12, 20)
+    np.testing.assert_allclose(dw, dy.astype(np.float64).T @ x.astype(np.float64),
+                               rtol=1e-5, atol=1e-5)
+    di = rng.integers(-4, 5, (33, 8)).astype(np.float32)
+    xi = rng.integers(-4, 5, (33, 16)).astype(np.float32)
+    assert np.array_equal(oracle.wgrad(di, xi), (di.astype(np.int64).T @ xi.astype(np.int64)))
+    # The micro-batch sum (backward.rs:478-502): dw += dy^T . x.
+    acc = oracle.wgrad(dy, x, np.ones((12, 20), np.float32))
+    np.testing.assert_allclose(acc, dw + 1, rtol=1e-5, atol=1e-5)
+
+
 def test_generator_statistics():
     x = oracle.gen_normal(42, 1 << 18, 0.02)
     assert abs(float(x.mean())) < 2e-4
