@@ -93,6 +93,10 @@ __device__ __forceinline__ void wg_read(const char *tdy, const char *tx, const u
 // barrier after MFMA 7 of sub-step 3 waits for every DMA and LDS read; the
 // last 8 MFMAs (operands in registers) open the next call, each followed by
 // one of the next step's sub-step 0 reads.
+// `more` (no next step) skips the DMAs of the tile's last step.  As a branch
+// it splits the step into basic blocks, which keeps each DMA after its
+// slot's MFMA and reads; a single-block variant with the DMAs unconditional
+// measured 2-3 % slower on 70B shapes.
 // The four LDS tiles come in as distinct __restrict__ pointers: the
 // compiler then knows that DMAs into the next stage never alias the reads of
 // the current one and waits (vmcnt) only at the barrier.

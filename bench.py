@@ -88,8 +88,10 @@ def parse():
                     help="only run a plain 1 GiB device-to-device copy (PMC byte calibration)")
     ap.add_argument("--gemm-shape", choices=sorted(GEMM_SHAPES), default=None,
                     help="only time one fused GEMM shape (for profiling)")
-    ap.add_argument("--gemm-mode", choices=["fwd", "dgrad", "bf16-reference"], default="fwd",
-                    help="bf16-reference: torch.matmul (hipBLASLt) of the same shape in bf16")
+    ap.add_argument("--gemm-mode", choices=["fwd", "dgrad", "wgrad", "bf16-reference"],
+                    default="fwd",
+                    help="wgrad: the weight gradient dW[n,k] = dy^T.x over m tokens (fp32 out); "
+                         "bf16-reference: torch.matmul (hipBLASLt) of the same shape in bf16")
     return ap.parse_args()
 
 
@@ -262,6 +264,15 @@ def bench_gemm(torch, nf4, gemm, args):
         fwd_pass()      # double-pass recompute forward
         dgrad_pass()    # input gradient
 
+    # The weight gradients beside the input gradients (backward.rs:87-93,
+    # 117-129, 160-168, 284-300): dW_i = dy_i^T . input_i in fp32, plain bf16
+    # GEMMs (no NF4 operand), reported apart from the NF4 path's rate.
+    dws = [torch.empty(w.shape[0], w.shape[1], dtype=torch.float32, device="cuda") for w in ws]
+
+    def wgrad_pass():
+        for dy, a, dw in zip(dys, ins, dws):
+            gemm.linear_wgrad(dy, a, dw)
+
     steps4 = max(2, args.steps // 10)
     ms_f = timed(torch, fwd_pass, steps4, 1, name="config4_fwd_pass")
     ms_d = timed(torch, dgrad_pass, steps4, 1, name="config4_dgrad_pass")
@@ -285,6 +296,7 @@ def bench_gemm(torch, nf4, gemm, args):
         gemm.linear_fwd(hsw, ws[6], ys[6])
 
     ms_fs = timed(torch, fwd_pass_swiglu, steps4, 1, name="config4_fwd_pass_swiglu")
+    ms_w = timed(torch, wgrad_pass, steps4, 1, name="config4_wgrad_pass")
     fl_gu = 2 * 2.0 * M * 28672 * 8192
     ms_gu = timed(torch, lambda: gemm.linear_fwd_grouped(h, ws[4:6], ys[4:6]), steps4, 1,
                   name="gate_up_grouped")
@@ -302,6 +314,7 @@ def bench_gemm(torch, nf4, gemm, args):
         "gate_up_grouped_tflops": round(fl_gu / (ms_gu * 1e-3) / 1e12, 1),
         "gate_up_swiglu_fused_tflops": round(fl_gu / (ms_sw * 1e-3) / 1e12, 1),
         "dgrad_pass_tflops": round(fl_pass / (ms_d * 1e-3) / 1e12, 1),
+        "wgrad_pass_tflops": round(fl_pass / (ms_w * 1e-3) / 1e12, 1),
         "per_matrix": per,
     }
     return res
@@ -397,6 +410,11 @@ def bench_one_gemm(torch, nf4, gemm, args):
         b = torch.randn(n, k, device="cuda", generator=g).to(torch.bfloat16)
         o = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
         fn = lambda: torch.matmul(a, b.t(), out=o)
+    elif args.gemm_mode == "wgrad":
+        a = torch.randn(m, n, device="cuda", generator=g).to(torch.bfloat16)
+        b = torch.randn(m, k, device="cuda", generator=g).to(torch.bfloat16)
+        o = torch.empty(n, k, dtype=torch.float32, device="cuda")
+        fn = lambda: gemm.linear_wgrad(a, b, o)
     else:
         a = torch.randn(m, n, device="cuda", generator=g).to(torch.bfloat16)
         o = torch.empty(m, k, dtype=torch.bfloat16, device="cuda")
