@@ -252,6 +252,14 @@ struct DqBatch {
 // waves each dequantized two rounds (32 KB per workgroup), and a write-only
 // fill shows the same preference (6.5 TB/s at 4 KB per workgroup, 5.3 TB/s
 // at 64 KB).
+// Cache policy: the packed nibbles load with the default policy (a
+// non-temporal load measured 6.13-6.32 TB/s against 6.83-6.85), and the
+// output goes out non-temporal and sc1 (kStoreNtSc1; 6.89-6.91 TB/s, nt
+// alone 6.83-6.85, the default policy 5.77-5.79).  The same access pattern
+// without the lookup work measured 6.90-6.91 TB/s: the lookup is hidden.
+// Buffer-instruction cache-policy bits on gfx950: nt (bit 1) | sc1 (bit 4).
+constexpr int kStoreNtSc1 = 2 | 16;
+
 template <bool kF16>
 __global__ void __launch_bounds__(kDqThreads) dequant_fast_kernel(const DqBatch batch) {
   __shared__ u32x4 stage[kDqWaves][64 * 4 + 4];  // per wave 4 KB, +1 pad unit per 16 lanes
@@ -267,10 +275,14 @@ __global__ void __launch_bounds__(kDqThreads) dequant_fast_kernel(const DqBatch 
   const int64_t nchunks = E.nchunks;
   if (cbase >= nchunks) return;  // wave-uniform
   const u32x4 *src = reinterpret_cast<const u32x4 *>(E.packed);
-  u32x4 *dst = reinterpret_cast<u32x4 *>(E.out);
+  // The wave's 64 chunks of output (4 KB) through a buffer resource, for the
+  // store's cache-policy bits; its size also bounds the stores.
+  const int64_t units = (nchunks - cbase < 64 ? nchunks - cbase : 64) * 4;
+  const __amdgpu_buffer_rsrc_t dst = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)(E.out + cbase * 32), 0, (int)(units * 16), 0x00020000);
   const int64_t c = cbase + lane;
   if (c < nchunks) {
-    const u32x4 w = __builtin_nontemporal_load(src + c);
+    const u32x4 w = src[c];
     const Lut16 lut = make_lut<kF16>(load_absmax(E.am, (c * 32) / E.block_size));
     const uint32_t words[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
@@ -287,8 +299,11 @@ __global__ void __launch_bounds__(kDqThreads) dequant_fast_kernel(const DqBatch 
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     const int u = k * 64 + lane;
-    if (cbase + (u >> 2) < nchunks)
-      __builtin_nontemporal_store(stage[wave][u + (u >> 6)], dst + cbase * 4 + u);
+    if (u < units) {
+      typedef unsigned int uvec4 __attribute__((ext_vector_type(4)));
+      __builtin_amdgcn_raw_buffer_store_b128(
+          __builtin_bit_cast(uvec4, stage[wave][u + (u >> 6)]), dst, u * 16, 0, kStoreNtSc1);
+    }
   }
 }
 
