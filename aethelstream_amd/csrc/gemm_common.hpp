@@ -75,7 +75,8 @@ __device__ __forceinline__ void map_tile(int b, int tiles_m, int tiles_o, int &t
 // output stores then drain while the same workgroup's next tile starts
 // loading.  The CU count is read once per device; a multiple of 8 keeps tile
 // b on XCD b % 8 (map_tile).
-inline uint32_t persistent_grid(int64_t tiles) {
+// The current device's compute-unit count rounded up to a multiple of 8.
+inline int cu_slots() {
   static std::atomic<int> cus[64];  // zero-initialized (static storage)
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
@@ -88,6 +89,11 @@ inline uint32_t persistent_grid(int64_t tiles) {
     c = (n + 7) & ~7;
     cus[dev].store(c, std::memory_order_relaxed);  // every caller stores the same value
   }
+  return c;
+}
+
+inline uint32_t persistent_grid(int64_t tiles) {
+  const int c = cu_slots();
   return (uint32_t)(tiles < c ? tiles : c);
 }
 

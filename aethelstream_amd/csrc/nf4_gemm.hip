@@ -49,6 +49,7 @@ struct GemmArgs {
   AbsmaxRef am;
   int64_t wk;         // columns of W (its k); W row stride = wk/2 bytes
   int64_t wn;         // rows of W (its n)
+  int64_t k0;         // first reduction step (a split-K slice's start; else 0)
   int32_t tiles_m, tiles_o;
 };
 
@@ -201,8 +202,8 @@ struct FwdProducer : FwdStore, PerStepLoads<kDQ, FwdProducer<kDQ>> {
     init_row();
     int64_t n = n0 + row;
     if (n >= g.wn) n = g.wn - 1;  // ragged N: clamp (outputs are not stored)
-    ptr = g.packed + n * (g.wk >> 1) + 16 * h;
-    am_idx = n * (g.wk >> 6);
+    ptr = g.packed + n * (g.wk >> 1) + 16 * h + 32 * g.k0;
+    am_idx = n * (g.wk >> 6) + g.k0;
     am = g.am;
   }
   __device__ __forceinline__ void load_step(const GemmArgs &g, int64_t step, u32x4 &w,
@@ -246,14 +247,14 @@ struct FwdBatchProducer : FwdStore {
     const int lane = threadIdx.x & 63;
     int64_t n = n0 + row;
     if (n >= g.wn) n = g.wn - 1;
-    am_idx = n * (g.wk >> 6);
+    am_idx = n * (g.wk >> 6) + g.k0;  // absolute block: scale groups stay aligned
     am = g.am;
     int64_t nx = n0 + 32 * (threadIdx.x >> 6) + (lane & 15);
     int64_t ny = nx + 16;
     if (nx >= g.wn) nx = g.wn - 1;
     if (ny >= g.wn) ny = g.wn - 1;
-    pkx = g.packed + nx * (g.wk >> 1) + 16 * (lane >> 4);
-    pky = g.packed + ny * (g.wk >> 1) + 16 * (lane >> 4);
+    pkx = g.packed + nx * (g.wk >> 1) + 16 * (lane >> 4) + 32 * g.k0;
+    pky = g.packed + ny * (g.wk >> 1) + 16 * (lane >> 4) + 32 * g.k0;
     npairs = g.R >> 7;
     ngroups = g.R >> 8;
   }
@@ -739,7 +740,19 @@ struct GroupedArgs {
   GemmGroup grp[kMaxGroups];
   int32_t ngroups;
   int32_t tiles_o;     // forward: output tiles over all groups
+  // Forward split-K tail: tiles [full_tiles, T) run as `splits` slices of
+  // `split_steps` reduction steps each, whose fp32 partial tiles go to `ws`
+  // (kPartialFloats per slice) and are summed by nf4_gemm_fixup_kernel.
+  int32_t full_tiles;  // T when there is no split
+  int32_t splits;
+  int32_t split_steps;
+  float *ws;
 };
+
+// One slice's partial tile: 256 threads x 256 accumulators, stored in the
+// accumulator register order, thread-interleaved in 16-byte units, so that
+// the fixup kernel's thread t reads back exactly thread t's values.
+constexpr int64_t kPartialFloats = (int64_t)kGemmThreads * 256;
 
 // Buffer resource and per-lane offsets of the wave's direct-to-LDS
 // activation loads: instruction i writes rows 8i..8i+7 of the wave's 128-row
@@ -753,7 +766,7 @@ struct GroupedArgs {
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t activation_setup(const GemmArgs &g, int64_t m0,
                                                                    int lane, uint32_t (&aoff)[16]) {
   const int64_t mb = (m0 < g.M) ? m0 : g.M - 1;
-  const char *abase = reinterpret_cast<const char *>(g.a + mb * g.lda);
+  const char *abase = reinterpret_cast<const char *>(g.a + mb * g.lda + kStep * g.k0);
   // Rows available to this wave from mb (at least 1, at most 128).
   const int64_t avail64 = g.M - mb;
   const int32_t avail = (int32_t)(avail64 > 128 ? 128 : avail64);
@@ -889,35 +902,60 @@ __device__ __forceinline__ void epilogue(const GemmArgs &g, const floatx16 (&acc
     store_tile(g, acc, m0, o0, lane & 31, lane >> 5);
 }
 
+// Output tile `tile` of a forward launch: its rows, its group's output and
+// weight, and its first output column.
+__device__ __forceinline__ void fwd_tile(const GroupedArgs &ga, int tile, GemmArgs &g, int64_t &m0,
+                                         int64_t &o0, int wave) {
+  g = ga.base;
+  int tm, to;
+  map_tile(tile, g.tiles_m, ga.tiles_o, tm, to);
+  // The group of output tile `to` (uniform; at most kMaxGroups iterations).
+  int gi = 0;
+  while (gi + 1 < ga.ngroups && to >= ga.grp[gi].tiles_o) {
+    to -= ga.grp[gi].tiles_o;
+    ++gi;
+  }
+  g.out = ga.grp[gi].out;
+  g.ldo = ga.grp[gi].ldo;
+  g.packed = ga.grp[gi].packed;
+  g.am = ga.grp[gi].am;
+  g.wn = ga.grp[gi].wn;
+  g.O = ga.grp[gi].wn;
+  m0 = (int64_t)tm * kTileM + wave * 128;
+  o0 = (int64_t)to * kTileO;
+}
+
 // Forward: y_i = x . W_i^T.  The grid covers tiles_m x (output tiles of all
 // groups); consecutive tiles share the activation rows (map_tile), also
-// across a group boundary.
+// across a group boundary.  Work unit b < full_tiles is tile b; the units
+// after it are the split-K slices of the remaining tiles (slice = unit %
+// splits), each over split_steps reduction steps from step slice *
+// split_steps, whose fp32 partials go to the workspace.
 template <class Producer>
 __global__ void __launch_bounds__(kGemmThreads, 1) nf4_gemm_fwd_kernel(const GroupedArgs ga) {
   const int T = ga.base.tiles_m * ga.tiles_o;
+  const int U = ga.full_tiles + (T - ga.full_tiles) * ga.splits;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int jl = lane & 31;
   const int grp = lane >> 5;
 #pragma unroll 1
-  for (int b = blockIdx.x; b < T; b += gridDim.x) {
-    GemmArgs g = ga.base;
-    int tm, to;
-    map_tile(b, g.tiles_m, ga.tiles_o, tm, to);
-    // The group of output tile `to` (uniform; at most kMaxGroups iterations).
-    int gi = 0;
-    while (gi + 1 < ga.ngroups && to >= ga.grp[gi].tiles_o) {
-      to -= ga.grp[gi].tiles_o;
-      ++gi;
+  for (int b = blockIdx.x; b < U; b += gridDim.x) {
+    int tile = b, slice = -1;
+    if (b >= ga.full_tiles) {
+      const int u = b - ga.full_tiles;
+      tile = ga.full_tiles + u / ga.splits;
+      slice = u - (u / ga.splits) * ga.splits;
     }
-    g.out = ga.grp[gi].out;
-    g.ldo = ga.grp[gi].ldo;
-    g.packed = ga.grp[gi].packed;
-    g.am = ga.grp[gi].am;
-    g.wn = ga.grp[gi].wn;
-    g.O = ga.grp[gi].wn;
-    const int64_t m0 = (int64_t)tm * kTileM + wave * 128;
-    const int64_t o0 = (int64_t)to * kTileO;
+    GemmArgs g;
+    int64_t m0, o0;
+    fwd_tile(ga, tile, g, m0, o0, wave);
+    if (slice >= 0) {
+      const int64_t steps = g.R / kStep;
+      g.k0 = (int64_t)slice * ga.split_steps;
+      const int64_t left = steps - g.k0;
+      g.R = kStep * (left < ga.split_steps ? left : ga.split_steps);
+    }
     uint32_t aoff[16];
     const __amdgpu_buffer_rsrc_t arsrc = activation_setup(g, m0, lane, aoff);
     Producer prod;
@@ -926,7 +964,77 @@ __global__ void __launch_bounds__(kGemmThreads, 1) nf4_gemm_fwd_kernel(const Gro
     zero_acc(acc);
     gemm_main<Producer>(g, prod, acc, &g_lds_a[wave][0][0], &g_lds_a[wave][1][0], g_lds_b[0],
                         g_lds_b[1], arsrc, aoff, g.R / kStep, jl, grp);
-    epilogue(g, acc, wave, m0, o0, lane);
+    if (slice < 0) {
+      epilogue(g, acc, wave, m0, o0, lane);
+    } else {
+      floatx4 *part = reinterpret_cast<floatx4 *>(
+          ga.ws + (int64_t)(b - ga.full_tiles) * kPartialFloats) + threadIdx.x;
+#pragma unroll
+      for (int i = 0; i < 64; ++i) {
+        const floatx16 &a = acc[i >> 4][(i >> 2) & 3];
+        const int v = 4 * (i & 3);
+        part[i * kGemmThreads] = (floatx4){a[v], a[v + 1], a[v + 2], a[v + 3]};
+      }
+    }
+  }
+}
+
+// Split-K fixup, launched after the main kernel on the same stream.  The
+// partials of a unit are [quad i = 0..63][thread t] floatx4, quad i holding
+// thread t's acc[i / 16][(i / 4) % 4][4 (i % 4) .. + 3]: 4 adjacent output
+// columns of one row.  Workgroup (j, q) sums quads kFixupQuads * q .. of tail
+// tile full_tiles + j over its `splits` slices in slice order (fp32) and
+// stores them as bf16, so that 16 workgroups per tile keep every CU loading.
+constexpr int kFixupQuads = 4;
+constexpr int kFixupBlocksPerTile = 64 / kFixupQuads;
+__global__ void __launch_bounds__(kGemmThreads) nf4_gemm_fixup_kernel(const GroupedArgs ga) {
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int j = blockIdx.x / kFixupBlocksPerTile;
+  const int q = blockIdx.x - j * kFixupBlocksPerTile;
+  GemmArgs g;
+  int64_t m0, o0;
+  fwd_tile(ga, ga.full_tiles + j, g, m0, o0, wave);
+  const bool vec_ok = ((reinterpret_cast<uintptr_t>(g.out) & 7) == 0) && ((g.ldo & 3) == 0);
+  const floatx4 *part = reinterpret_cast<const floatx4 *>(ga.ws + (int64_t)j * ga.splits *
+                                                                      kPartialFloats) +
+                        threadIdx.x;
+  // All quads of a slice are loaded before any is added, so each thread has
+  // kFixupQuads (x2 with the unroll) loads in flight rather than one.
+  floatx4 acc[kFixupQuads];
+#pragma unroll
+  for (int ii = 0; ii < kFixupQuads; ++ii) acc[ii] = (floatx4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll 2
+  for (int sl = 0; sl < ga.splits; ++sl) {
+    floatx4 p[kFixupQuads];
+#pragma unroll
+    for (int ii = 0; ii < kFixupQuads; ++ii)
+      p[ii] = part[(int64_t)sl * (kPartialFloats / 4) + (q * kFixupQuads + ii) * kGemmThreads];
+#pragma unroll
+    for (int ii = 0; ii < kFixupQuads; ++ii) {
+      acc[ii][0] += p[ii][0];
+      acc[ii][1] += p[ii][1];
+      acc[ii][2] += p[ii][2];
+      acc[ii][3] += p[ii][3];
+    }
+  }
+#pragma unroll
+  for (int ii = 0; ii < kFixupQuads; ++ii) {
+    const int i = q * kFixupQuads + ii;
+    const int64_t m = m0 + 32 * (i >> 4) + (lane & 31);
+    const int64_t c = o0 + 4 * (lane >> 5) + 32 * ((i >> 2) & 3) + 8 * (i & 3);
+    if (m >= g.M || c >= g.O) continue;
+    uint16_t *o = g.out + m * g.ldo + c;
+    const uint32_t lo = pack_bf16x2(acc[ii][0], acc[ii][1]);
+    const uint32_t hi = pack_bf16x2(acc[ii][2], acc[ii][3]);
+    if (vec_ok && c + 4 <= g.O) {
+      *reinterpret_cast<u32x2 *>(o) = (u32x2){lo, hi};
+    } else {
+      o[0] = (uint16_t)(lo & 0xffffu);
+      if (c + 1 < g.O) o[1] = (uint16_t)(lo >> 16);
+      if (c + 2 < g.O) o[2] = (uint16_t)(hi & 0xffffu);
+      if (c + 3 < g.O) o[3] = (uint16_t)(hi >> 16);
+    }
   }
 }
 
@@ -1110,14 +1218,64 @@ static GemmGroup group_of(const nf4s_tensor &w, int64_t wn) {
   return q;
 }
 
+// Split-K plan for a forward launch of T tiles and `nsteps` reduction steps.
+// A last round of r tiles (0 < r <= half the CUs) runs as S = CUs / r
+// slices per tile, so that it fills the chip; every slice keeps at least
+// `unroll` steps (and a multiple of them).  Returns the partial-tile count
+// r * S, or 0 for no split.
+struct SplitPlan {
+  int64_t tail_tiles, splits, split_steps;
+};
+static SplitPlan split_plan(int64_t T, int64_t nsteps, int unroll) {
+  SplitPlan p{0, 1, 0};
+  const int64_t cus = cu_slots();
+  const int64_t r = T % cus;
+  if (r == 0 || 2 * r > cus) return p;
+  int64_t S = cus / r;
+  if (S > nsteps / unroll) S = nsteps / unroll;
+  if (S < 2) return p;
+  int64_t per = (nsteps + S - 1) / S;
+  per = (per + unroll - 1) / unroll * unroll;
+  S = (nsteps + per - 1) / per;
+  if (S < 2) return p;
+  p.tail_tiles = r;
+  p.splits = S;
+  p.split_steps = per;
+  return p;
+}
+
+// Workspace bytes a split plan needs (0 without a split).
+static int64_t split_bytes(const SplitPlan &p) {
+  return p.tail_tiles * p.splits * kPartialFloats * (int64_t)sizeof(float);
+}
+
 template <class Producer>
-static int32_t launch_fwd(const GroupedArgs &ga, hipStream_t s) {
+static int32_t launch_fwd(GroupedArgs &ga, hipStream_t s, void *ws, int64_t ws_bytes) {
   const int64_t T = (int64_t)ga.base.tiles_m * ga.tiles_o;
   if (T == 0) return NF4S_OK;
   if (T > 0x7fffffff) return fail(NF4S_ERR_UNSUPPORTED_SHAPE, "too many tiles");
-  hipLaunchKernelGGL(nf4_gemm_fwd_kernel<Producer>, dim3(persistent_grid(T)), dim3(kGemmThreads),
+  ga.full_tiles = (int32_t)T;
+  ga.splits = 1;
+  ga.split_steps = 0;
+  ga.ws = nullptr;
+  const SplitPlan p = split_plan(T, ga.base.R / kStep, Producer::kUnroll);
+  if (ws != nullptr && p.tail_tiles > 0 && ws_bytes >= split_bytes(p)) {
+    ga.full_tiles = (int32_t)(T - p.tail_tiles);
+    ga.splits = (int32_t)p.splits;
+    ga.split_steps = (int32_t)p.split_steps;
+    ga.ws = static_cast<float *>(ws);
+  }
+  const int64_t U = ga.full_tiles + (T - ga.full_tiles) * ga.splits;
+  hipLaunchKernelGGL(nf4_gemm_fwd_kernel<Producer>, dim3(persistent_grid(U)), dim3(kGemmThreads),
                      0, s, ga);
-  return check_launch("nf4_gemm_fwd");
+  int32_t rc = check_launch("nf4_gemm_fwd");
+  if (rc == NF4S_OK && ga.splits > 1) {
+    hipLaunchKernelGGL(nf4_gemm_fixup_kernel,
+                       dim3((uint32_t)((T - ga.full_tiles) * kFixupBlocksPerTile)),
+                       dim3(kGemmThreads), 0, s, ga);
+    rc = check_launch("nf4_gemm_fixup");
+  }
+  return rc;
 }
 
 template <class Producer>
@@ -1135,7 +1293,7 @@ static int32_t launch_dgrad(const GroupedArgs &ga, hipStream_t s) {
 // a launch; a mixed set runs as one launch per kind.
 static int32_t gemm_fwd_groups(const uint16_t *x, const nf4s_tensor *ws, const int64_t *ns,
                                uint16_t *const *ys, int32_t count, int64_t m, int64_t k,
-                               hipStream_t s) {
+                               hipStream_t s, void *work = nullptr, int64_t work_bytes = 0) {
   if (count <= 0 || count > kMaxGroups)
     return fail(NF4S_ERR_INVALID_ARGUMENT, "count must be 1..%d, got %d", kMaxGroups, count);
   if (ws == nullptr || ns == nullptr || ys == nullptr)
@@ -1175,10 +1333,10 @@ static int32_t gemm_fwd_groups(const uint16_t *x, const nf4s_tensor *ws, const i
     if (tiles > 0x7fffffff) return fail(NF4S_ERR_UNSUPPORTED_SHAPE, "too many tiles");
     ga.tiles_o = (int32_t)tiles;
     switch (kind[i]) {
-      case 3: rc = launch_fwd<FwdBatchProducer<true>>(ga, s); break;
-      case 2: rc = launch_fwd<FwdBatchProducer<false>>(ga, s); break;
-      case 1: rc = launch_fwd<FwdProducer<true>>(ga, s); break;
-      default: rc = launch_fwd<FwdProducer<false>>(ga, s); break;
+      case 3: rc = launch_fwd<FwdBatchProducer<true>>(ga, s, work, work_bytes); break;
+      case 2: rc = launch_fwd<FwdBatchProducer<false>>(ga, s, work, work_bytes); break;
+      case 1: rc = launch_fwd<FwdProducer<true>>(ga, s, work, work_bytes); break;
+      default: rc = launch_fwd<FwdProducer<false>>(ga, s, work, work_bytes); break;
     }
     if (rc != NF4S_OK) return rc;
   }
@@ -1297,6 +1455,44 @@ int32_t nf4s_gemm_fwd_grouped(const uint16_t *x, const nf4s_tensor *ws, const in
                               uint16_t *const *ys, int32_t count, int64_t m, int64_t k,
                               void *stream) {
   return gemm_fwd_groups(x, ws, ns, ys, count, m, k, as_stream(stream));
+}
+
+int32_t nf4s_gemm_fwd_grouped_ws(const uint16_t *x, const nf4s_tensor *ws, const int64_t *ns,
+                                 uint16_t *const *ys, int32_t count, int64_t m, int64_t k,
+                                 void *workspace, int64_t workspace_bytes, void *stream) {
+  if (workspace_bytes < 0)
+    return fail(NF4S_ERR_INVALID_ARGUMENT, "negative workspace size %lld",
+                (long long)workspace_bytes);
+  if (workspace != nullptr && !aligned(workspace, 16))
+    return fail(NF4S_ERR_MISALIGNED, "workspace must be 16-byte aligned");
+  return gemm_fwd_groups(x, ws, ns, ys, count, m, k, as_stream(stream), workspace,
+                         workspace_bytes);
+}
+
+int32_t nf4s_gemm_fwd_workspace_size(const int64_t *ns, int32_t count, int64_t m, int64_t k,
+                                     int64_t *bytes) {
+  if (bytes == nullptr) return fail(NF4S_ERR_INVALID_ARGUMENT, "bytes is NULL");
+  *bytes = 0;
+  if (count <= 0 || count > kMaxGroups || ns == nullptr)
+    return fail(NF4S_ERR_INVALID_ARGUMENT, "count must be 1..%d with sizes", kMaxGroups);
+  // Shapes the GEMM itself rejects need no workspace; the GEMM call reports
+  // them with its own message.
+  if (m <= 0 || k <= 0 || k % 64 != 0) return NF4S_OK;
+  int64_t tiles_o = 0;
+  for (int32_t i = 0; i < count; ++i) {
+    if (ns[i] <= 0) return NF4S_OK;
+    tiles_o += (ns[i] + kTileO - 1) / kTileO;
+  }
+  // The plan of one launch over all the weights (weights of one kind), the
+  // larger of the two producers' step multiples.  A mixed set runs one
+  // launch per kind; a launch whose plan needs more than the workspace
+  // given runs without a split.
+  const int64_t T = (m + kTileM - 1) / kTileM * tiles_o;
+  if (T == 0) return NF4S_OK;
+  const int64_t a = split_bytes(split_plan(T, k / kStep, 2));
+  const int64_t b = split_bytes(split_plan(T, k / kStep, 4));
+  *bytes = a > b ? a : b;
+  return NF4S_OK;
 }
 
 int32_t nf4s_gemm_fwd_swiglu(const uint16_t *x, const nf4s_tensor *w_gate,

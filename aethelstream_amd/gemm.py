@@ -37,9 +37,14 @@ def _check_act(t: torch.Tensor, cols: int, name: str) -> None:
         raise ValueError(f"{name} must be [M, {cols}], got {list(t.shape)}")
 
 
-def linear_fwd(x: torch.Tensor, w: Nf4Weight, out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """y[M, N] = x[M, K] . W[N, K]^T (bf16 in/out, fp32 accumulate)."""
+def linear_fwd(x: torch.Tensor, w: Nf4Weight, out: Optional[torch.Tensor] = None,
+               split_k: bool = True) -> torch.Tensor:
+    """y[M, N] = x[M, K] . W[N, K]^T (bf16 in/out, fp32 accumulate).  With
+    ``split_k`` a last round that would leave most CUs idle runs as split-K
+    slices (nf4s_gemm_fwd_grouped_ws)."""
     n, k = int(w.shape[0]), int(w.shape[1])
+    if split_k:
+        return linear_fwd_grouped(x, [w], None if out is None else [out], split_k=True)[0]
     _check_act(x, k, "x")
     m = x.shape[0]
     if out is None:
@@ -73,9 +78,22 @@ def _descs(ws: Sequence[Nf4Weight]):
     return arr
 
 
+def fwd_workspace_bytes(ns: Sequence[int], m: int, k: int) -> int:
+    """Workspace nf4s_gemm_fwd_grouped_ws uses for these shapes (0: no split)."""
+    arr = (ctypes.c_int64 * len(ns))(*[int(v) for v in ns])
+    out = ctypes.c_int64(0)
+    _lib.check(_lib.load().nf4s_gemm_fwd_workspace_size(arr, len(ns), m, k, ctypes.byref(out)))
+    return int(out.value)
+
+
 def linear_fwd_grouped(x: torch.Tensor, ws: Sequence[Nf4Weight],
-                       outs: Optional[Sequence[torch.Tensor]] = None) -> List[torch.Tensor]:
-    """[x . W_i^T for W_i in ws] (1..4 weights of one k) in one launch."""
+                       outs: Optional[Sequence[torch.Tensor]] = None, split_k: bool = True,
+                       workspace: Optional[torch.Tensor] = None) -> List[torch.Tensor]:
+    """[x . W_i^T for W_i in ws] (1..4 weights of one k) in one launch.  With
+    ``split_k`` a last round that would leave most CUs idle runs as split-K
+    slices whose fp32 partials go to ``workspace`` (by default a buffer from
+    torch's caching allocator on x's stream, so calls on other streams never
+    share it)."""
     if not 1 <= len(ws) <= 4:
         raise ValueError("linear_fwd_grouped takes 1 to 4 weights")
     k = int(ws[0].shape[1])
@@ -93,8 +111,17 @@ def linear_fwd_grouped(x: torch.Tensor, ws: Sequence[Nf4Weight],
     ns = (ctypes.c_int64 * len(ws))(*[int(w.shape[0]) for w in ws])
     ys = (ctypes.c_void_p * len(ws))(*[o.data_ptr() for o in outs])
     descs = _descs(ws)
-    _lib.check(_lib.load().nf4s_gemm_fwd_grouped(x.data_ptr(), descs, ns, ys, len(ws), m, k,
-                                                 _stream_ptr(x)))
+    need = fwd_workspace_bytes(list(ns), m, k) if split_k else 0
+    if need > 0:
+        if workspace is None or workspace.numel() * workspace.element_size() < need:
+            workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
+        _require_cuda(workspace)
+        _lib.check(_lib.load().nf4s_gemm_fwd_grouped_ws(
+            x.data_ptr(), descs, ns, ys, len(ws), m, k, workspace.data_ptr(),
+            workspace.numel() * workspace.element_size(), _stream_ptr(x)))
+    else:
+        _lib.check(_lib.load().nf4s_gemm_fwd_grouped(x.data_ptr(), descs, ns, ys, len(ws), m, k,
+                                                     _stream_ptr(x)))
     return list(outs)
 
 

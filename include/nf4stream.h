@@ -201,6 +201,27 @@ int32_t nf4s_gemm_dgrad_sum(const uint16_t *const *dys, const nf4s_tensor *ws,
                             int64_t k, uint16_t *dx, void *stream);
 
 /*
+ * nf4s_gemm_fwd_grouped with a workspace for a split-K last round.  When the
+ * output tiles leave a last round of r tiles on fewer than half the compute
+ * units, each of those tiles runs as S = CUs / r slices of its reduction,
+ * whose fp32 partial tiles go to `workspace` and are summed (in slice order)
+ * by a second kernel on the same stream.  No counterpart in the reference:
+ * it only reorders matmul_tb's fp32 sum (doublepass/src/math.rs:9-21).
+ * workspace may be NULL or smaller than nf4s_gemm_fwd_workspace_size
+ * reports: the call then runs without the split.  Calls that share a
+ * workspace must not overlap (one stream, or ordered streams).
+ */
+int32_t nf4s_gemm_fwd_grouped_ws(const uint16_t *x, const nf4s_tensor *ws,
+                                 const int64_t *ns, uint16_t *const *ys,
+                                 int32_t count, int64_t m, int64_t k,
+                                 void *workspace, int64_t workspace_bytes,
+                                 void *stream);
+/* Workspace bytes nf4s_gemm_fwd_grouped_ws uses for these shapes on the
+ * current device (0: no split would help).  Allocates nothing. */
+int32_t nf4s_gemm_fwd_workspace_size(const int64_t *ns, int32_t count, int64_t m,
+                                     int64_t k, int64_t *bytes);
+
+/*
  * Weight gradient, bf16 in, fp32 out: dw[n, k] = sum_m dy[m, n] * x[m, k]
  * (accumulate = 0), or dw += that sum (accumulate != 0).  Replaces the d_wd,
  * d_wg / d_wu, d_wo and d_wq / d_wk / d_wv loops of single_layer_backward

@@ -85,6 +85,39 @@ def test_wgrad_argument_rejection():
     assert f(0x1000, 0x1000, 1 << 20, 1024, 64, 0x1000, 0, None) == _lib.NF4S_ERR_UNSUPPORTED_SHAPE
 
 
+def test_fwd_workspace_size_query():
+    """The split-K workspace query allocates nothing and needs no kernel.  On a
+    host without a GPU the CU count reads as 256, the MI355X's."""
+    lib = _lib.load()
+    f = lib.nf4s_gemm_fwd_workspace_size
+    out = ctypes.c_int64(-1)
+    ns = (ctypes.c_int64 * 4)(1024, 1024, 1024, 1024)
+    assert f(ns, 1, 8192, 8192, None) == _lib.NF4S_ERR_INVALID_ARGUMENT
+    assert f(ns, 0, 8192, 8192, ctypes.byref(out)) == _lib.NF4S_ERR_INVALID_ARGUMENT
+    assert f(ns, 5, 8192, 8192, ctypes.byref(out)) == _lib.NF4S_ERR_INVALID_ARGUMENT
+    # k % 64 != 0 is the GEMM's own error; the query just reports no split.
+    assert f(ns, 1, 8192, 96, ctypes.byref(out)) == 0 and out.value == 0
+    if torch_has_gpu():
+        return
+    # 8192 x 1024 outputs = 128 tiles of 512 x 128: half a round of 256 CUs,
+    # so two K slices of 256 x 256 fp32 partials (256 KiB) per tile.
+    assert f(ns, 1, 8192, 8192, ctypes.byref(out)) == 0
+    assert out.value == 128 * 2 * 256 * 1024
+    # 8192 x 8192 = 1024 tiles: whole rounds, no split.
+    ns[0] = 8192
+    assert f(ns, 1, 8192, 8192, ctypes.byref(out)) == 0 and out.value == 0
+    # A negative workspace size is rejected before any launch.
+    assert lib.nf4s_gemm_fwd_grouped_ws(0x1000, None, ns, None, 1, 64, 64, None, -1,
+                                        None) == _lib.NF4S_ERR_INVALID_ARGUMENT
+    assert lib.nf4s_gemm_fwd_grouped_ws(0x1000, None, ns, None, 1, 64, 64, 0x1008, 64,
+                                        None) == _lib.NF4S_ERR_MISALIGNED
+
+
+def torch_has_gpu():
+    import torch
+    return torch.cuda.is_available()
+
+
 def test_python_mirror_raises_malformed_index():
     import torch
     from aethelstream_amd import nf4

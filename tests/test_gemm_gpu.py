@@ -7,12 +7,14 @@ north_star tolerance); and against fp32 on the same bf16 operands, rel-L2 <=
 4e-3 (bf16 output rounding only).  Layer shapes (7B, 70B): against a torch
 fp32 GPU matmul over the bit-checked bf16 dequantized weights, plus sampled
 rows in fp64 on the CPU."""
+import ctypes
+
 import numpy as np
 import pytest
 import torch
 
 import oracle
-from aethelstream_amd import gemm, nf4
+from aethelstream_amd import _lib, gemm, nf4
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -105,13 +107,13 @@ def test_fwd_batched_equals_per_step(m, n, k, dq):
     # kernel.  Same products, same reduction order: bit-identical outputs.
     w = _weight(n, k, 41 + n + k, dq)
     x, _ = _act(m, k, 13 + m)
-    y_batched = gemm.linear_fwd(x, w)
+    y_batched = gemm.linear_fwd(x, w, split_k=False)
     if dq:
         w2 = nf4.Nf4Weight(packed=w.packed, absmax=None, shape=w.shape, absmax_q=_misaligned(w.absmax_q, 1),
                            absmax_scale=w.absmax_scale, dq_group=w.dq_group)
     else:
         w2 = nf4.Nf4Weight(packed=w.packed, absmax=_misaligned(w.absmax, 1), shape=w.shape)
-    y_step = gemm.linear_fwd(x, w2)
+    y_step = gemm.linear_fwd(x, w2, split_k=False)
     torch.cuda.synchronize()
     assert torch.equal(y_batched.view(torch.int16), y_step.view(torch.int16))
 
@@ -215,8 +217,8 @@ def test_gemm_argument_errors():
 def test_fwd_grouped_equals_separate(m, k, ns, dqs):
     ws = [_weight(n, k, 51 + i * 7 + n, dq) for i, (n, dq) in enumerate(zip(ns, dqs))]
     x, _ = _act(m, k, 17 + m)
-    ys = gemm.linear_fwd_grouped(x, ws)
-    sep = [gemm.linear_fwd(x, w) for w in ws]
+    ys = gemm.linear_fwd_grouped(x, ws, split_k=False)
+    sep = [gemm.linear_fwd(x, w, split_k=False) for w in ws]
     torch.cuda.synchronize()
     for y, s in zip(ys, sep):
         assert torch.equal(y.view(torch.int16), s.view(torch.int16))
@@ -318,3 +320,69 @@ def test_swiglu_argument_errors():
         gemm.linear_swiglu(x, w, wq)
     with pytest.raises(ValueError):
         gemm.linear_swiglu(x, w, _weight(64, 128, 4))
+
+
+# Split-K last round (nf4s_gemm_fwd_grouped_ws): tiles of a last round that
+# would leave most CUs idle run as K slices; the fixup kernel sums their fp32
+# partials in slice order.  Only the fp32 summation order changes, so both the
+# split and the unsplit result stay within TOL_SAME of fp32 on the same
+# operands.  Shapes (on a 256-CU MI355X): T = 100 tiles -> 2 slices; 16 tiles
+# of ragged M and N -> 8 slices of 4 steps; the per-step producer with an odd
+# step count; a 7B gate/up pair (1376 tiles, the last 96 split in 2); 70B k
+# alone (128 tiles).
+SPLIT = [(512, [12800], 1024, True), (513, [1000], 2048, True), (512, [3840], 1344, False),
+         (512, [3840], 1344, True), (4096, [11008, 11008], 4096, True),
+         (8192, [1024], 8192, True), (700, [3000, 1200], 512, False)]
+
+
+@pytest.mark.parametrize("m,ns,k,dq", SPLIT)
+def test_fwd_split_k_tail(m, ns, k, dq):
+    print(f"split-K m={m} ns={ns} k={k} dq={dq}", flush=True)
+    need = gemm.fwd_workspace_bytes(ns, m, k)
+    ws = [_weight(n, k, 61 + n + i, dq) for i, n in enumerate(ns)]
+    x, xf = _act(m, k, 19 + m)
+    ys = gemm.linear_fwd_grouped(x, ws, split_k=True)
+    ref = gemm.linear_fwd_grouped(x, ws, split_k=False)
+    torch.cuda.synchronize()
+    for w, y, r in zip(ws, ys, ref):
+        wdq = nf4.dequant(w).float()
+        exact = x.float() @ wdq.t()
+        torch.cuda.synchronize()
+        e_split = float((y.float() - exact).norm() / exact.norm())
+        e_ref = float((r.float() - exact).norm() / exact.norm())
+        assert e_split <= TOL_SAME and e_ref <= TOL_SAME, (e_split, e_ref)
+    if torch.cuda.get_device_properties(0).multi_processor_count == 256:
+        assert need > 0  # these shapes do split on a 256-CU part
+
+
+def test_fwd_split_k_small_workspace_falls_back():
+    """A workspace smaller than one tile's partial sums, handed straight to the
+    C entry point (the Python wrapper would replace it): no split, the unsplit
+    result bit for bit."""
+    m, n, k = 512, 12800, 1024
+    w = _weight(n, k, 71, True)
+    x, _ = _act(m, k, 23)
+    small = torch.empty(4096, dtype=torch.uint8, device=DEV)
+    y = torch.empty(m, n, dtype=torch.bfloat16, device=DEV)
+    ns = (ctypes.c_int64 * 1)(n)
+    ys = (ctypes.c_void_p * 1)(y.data_ptr())
+    descs = (_lib.Nf4sTensor * 1)(w.descriptor())
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    _lib.check(_lib.load().nf4s_gemm_fwd_grouped_ws(x.data_ptr(), descs, ns, ys, 1, m, k,
+                                                    small.data_ptr(), 4096, stream))
+    r = gemm.linear_fwd(x, w, split_k=False)
+    torch.cuda.synchronize()
+    assert torch.equal(y.view(torch.int16), r.view(torch.int16))
+
+
+def test_fwd_split_k_twice_in_a_row():
+    """Two split launches on one stream reuse one workspace: the second (a
+    smaller shape) must not see the first's partials."""
+    ws_buf = torch.empty(64 << 20, dtype=torch.uint8, device=DEV)
+    for m, n, k, seed in ((512, 12800, 1024, 81), (256, 6400, 512, 82)):
+        w = _weight(n, k, seed, True)
+        x, _ = _act(m, k, seed)
+        y = gemm.linear_fwd_grouped(x, [w], split_k=True, workspace=ws_buf)[0]
+        exact = x.float() @ nf4.dequant(w).float().t()
+        torch.cuda.synchronize()
+        assert float((y.float() - exact).norm() / exact.norm()) <= TOL_SAME
