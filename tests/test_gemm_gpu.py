@@ -329,17 +329,20 @@ def test_swiglu_argument_errors():
 # operands.  Shapes (on a 256-CU MI355X): T = 100 tiles -> 2 slices; 16 tiles
 # of ragged M and N -> 8 slices of 4 steps; the per-step producer with an odd
 # step count; a 7B gate/up pair (1376 tiles, the last 96 split in 2); 70B k
-# alone (128 tiles).
+# alone (128 tiles); a group mixing double-quant and fp32-absmax weights, which
+# runs one launch per kind over one workspace.
 SPLIT = [(512, [12800], 1024, True), (513, [1000], 2048, True), (512, [3840], 1344, False),
          (512, [3840], 1344, True), (4096, [11008, 11008], 4096, True),
-         (8192, [1024], 8192, True), (700, [3000, 1200], 512, False)]
+         (8192, [1024], 8192, True), (700, [3000, 1200], 512, False),
+         (512, [6400, 1000, 6400], 1024, (True, False, False))]
 
 
 @pytest.mark.parametrize("m,ns,k,dq", SPLIT)
 def test_fwd_split_k_tail(m, ns, k, dq):
     print(f"split-K m={m} ns={ns} k={k} dq={dq}", flush=True)
     need = gemm.fwd_workspace_bytes(ns, m, k)
-    ws = [_weight(n, k, 61 + n + i, dq) for i, n in enumerate(ns)]
+    dqs = dq if isinstance(dq, tuple) else (dq,) * len(ns)
+    ws = [_weight(n, k, 61 + n + i, d) for i, (n, d) in enumerate(zip(ns, dqs))]
     x, xf = _act(m, k, 19 + m)
     ys = gemm.linear_fwd_grouped(x, ws, split_k=True)
     ref = gemm.linear_fwd_grouped(x, ws, split_k=False)
