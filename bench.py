@@ -7,6 +7,10 @@ an fp32 scale), one grouped launch per step, inputs resident in HBM.
 ``value`` = algorithmic bytes (packed + uint8 absmax + fp32 scales + bf16 out
 = 509,149,440 B) / average kernel time (HIP events on the launch stream), GB/s.
 
+"dequant_host_roundtrip": the same layer through the reference's host-slice
+API (fp32 absmax in, f16 out, both in pinned host memory): H2D + dequant + D2H
+per matrix on one stream, the PCIe-inclusive rate (never ``value``).
+
 Also reported under "gemm": the NF4-dequant-fused GEMM in TFLOP/s against the
 bf16 dense MFMA peak,
   config 3: 4096 tokens x (gate, up 11008x4096; down 4096x11008), forward;
@@ -204,6 +208,45 @@ def bench_dequant(torch, nf4, args):
     ms = timed(torch, lambda: nf4.dequant_batch(ws, outs), args.steps, args.warmup,
                name="config2_dequant")
     return ws, ms
+
+
+def bench_dequant_host(torch, nf4, args):
+    """PCIe-inclusive rate of the reference's host-slice API (nf4.rs:37-83:
+    packed and absmax in host memory, f16 out to host memory) as the Rust
+    `hip` body runs it: per matrix of the 7B layer, H2D copy of packed bytes
+    and fp32 absmax (the reference's on-disk format), the f16 dequant, D2H
+    copy of the output; pinned host buffers, device staging kept, one stream.
+    Not the headline: the headline's inputs are already resident in HBM."""
+    g = torch.Generator(device="cuda").manual_seed(3)
+    mats = []
+    for _, r, c in LAYER_7B:
+        w = nf4.quantize_weight(torch.randn(r, c, device="cuda", generator=g) * 0.02,
+                                double_quant=False)
+        n = r * c
+        ph = torch.empty(w.packed.numel(), dtype=torch.uint8, pin_memory=True)
+        ah = torch.empty(w.absmax.numel(), dtype=torch.float32, pin_memory=True)
+        ph.copy_(w.packed)
+        ah.copy_(w.absmax)
+        oh = torch.empty(n, dtype=torch.float16, pin_memory=True)
+        od = torch.empty(n, dtype=torch.float16, device="cuda")
+        mats.append((ph, ah, oh, w.packed, w.absmax, od))
+    torch.cuda.synchronize()
+
+    def step():
+        for ph, ah, oh, pd, ad, od in mats:
+            pd.copy_(ph, non_blocking=True)
+            ad.copy_(ah, non_blocking=True)
+            nf4.dequant_nf4_into(pd, ad, od, 64)
+            oh.copy_(od, non_blocking=True)
+
+    ms = timed(torch, step, max(2, args.steps // 10), 1, name="dequant_host_roundtrip")
+    n_el = sum(r * c for _, r, c in LAYER_7B)
+    alg = n_el // 2 + 4 * (n_el // 64) + 2 * n_el
+    return {"gbs": round(alg / (ms * 1e-3) / 1e9, 2), "ms": round(ms, 3),
+            "algorithmic_bytes": alg, "h2d_bytes": n_el // 2 + 4 * (n_el // 64),
+            "d2h_bytes": 2 * n_el,
+            "note": "7B layer, fp32 absmax, f16 out; per matrix H2D + dequant + D2H on one "
+                    "stream, pinned host buffers"}
 
 
 def bench_gemm(torch, nf4, gemm, args):
@@ -505,6 +548,8 @@ def main():
         line["roofline"] = {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
                             "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
                             "traffic": read_traffic()}
+        log("PCIe-inclusive host-slice dequant")
+        line["dequant_host_roundtrip"] = bench_dequant_host(torch, nf4, args)
     if args.workload in ("all", "gemm"):
         line["gemm"] = bench_gemm(torch, nf4, gemm, args)
         line["gemm"]["peak_tflops"] = BF16_PEAK_TFLOPS
