@@ -113,9 +113,13 @@ def linear_fwd_grouped(x: torch.Tensor, ws: Sequence[Nf4Weight],
     descs = _descs(ws)
     need = fwd_workspace_bytes(list(ns), m, k) if split_k else 0
     if need > 0:
+        if workspace is not None and workspace.device != x.device:
+            raise ValueError("workspace must be on x's device")
         if workspace is None or workspace.numel() * workspace.element_size() < need:
             workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
         _require_cuda(workspace)
+        if not workspace.is_contiguous():
+            raise ValueError("workspace must be contiguous")
         _lib.check(_lib.load().nf4s_gemm_fwd_grouped_ws(
             x.data_ptr(), descs, ns, ys, len(ws), m, k, workspace.data_ptr(),
             workspace.numel() * workspace.element_size(), _stream_ptr(x)))
