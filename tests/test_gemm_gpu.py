@@ -389,3 +389,34 @@ def test_fwd_split_k_twice_in_a_row():
         exact = x.float() @ nf4.dequant(w).float().t()
         torch.cuda.synchronize()
         assert float((y.float() - exact).norm() / exact.norm()) <= TOL_SAME
+
+
+# Seeded random shapes: ragged m, any n for the forward (n % 64 == 0 for the
+# input gradient), k a multiple of 64 (per-step and batched producers), both
+# absmax formats, the forward with its default split-K.  Each against torch
+# fp32 over the same bf16 operands and the dequantized weight.
+RANDOM_CASES = 16
+
+
+@pytest.mark.parametrize("case", range(RANDOM_CASES))
+def test_random_shapes_fwd_and_dgrad(case):
+    rng = np.random.default_rng(9100 + case)
+    m = int(rng.integers(1, 2049))
+    k = 64 * int(rng.integers(1, 65))
+    n_fwd = int(rng.integers(1, 3073))
+    n_dg = 64 * int(rng.integers(1, 49))
+    dq = bool(rng.integers(0, 2))
+    print(f"random case {case}: m={m} k={k} n_fwd={n_fwd} n_dgrad={n_dg} dq={dq}", flush=True)
+    x, _ = _act(m, k, 300 + case)
+    w = _weight(n_fwd, k, 400 + case, dq)
+    y = gemm.linear_fwd(x, w)
+    ref = x.float() @ nf4.dequant(w).float().t()
+    torch.cuda.synchronize()
+    assert rel_l2(y.float().cpu().numpy(), ref.cpu().numpy()) <= TOL_SAME
+    wd = _weight(n_dg, k, 500 + case, dq)
+    dy, _ = _act(m, n_dg, 600 + case)
+    dx = gemm.linear_dgrad(dy, wd)
+    ref = dy.float() @ nf4.dequant(wd).float()
+    torch.cuda.synchronize()
+    assert rel_l2(dx.float().cpu().numpy(), ref.cpu().numpy()) <= TOL_SAME
+
