@@ -33,7 +33,7 @@ hipBLASLt) of the 70B gate shape on the same box, and what an unfused path
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
                        [--workload all|dequant|gemm|stream] [--stream-layers L]
                        [--copy-calibration]
-                       [--gemm-shape NAME [--gemm-mode fwd|dgrad]]
+                       [--gemm-shape NAME [--gemm-mode fwd|dgrad|wgrad|swiglu]]
   --gemm-shape times one fused GEMM (70b_q, 70b_k, 70b_gate, 70b_down, 7b_gate,
   7b_down) `steps` times after `warmup` and prints only its line (profiling);
   --gemm-mode bf16-reference times torch.matmul in bf16 on that shape instead.
@@ -92,7 +92,7 @@ def parse():
                     help="only run a plain 1 GiB device-to-device copy (PMC byte calibration)")
     ap.add_argument("--gemm-shape", choices=sorted(GEMM_SHAPES), default=None,
                     help="only time one fused GEMM shape (for profiling)")
-    ap.add_argument("--gemm-mode", choices=["fwd", "dgrad", "wgrad", "bf16-reference"],
+    ap.add_argument("--gemm-mode", choices=["fwd", "dgrad", "wgrad", "swiglu", "bf16-reference"],
                     default="fwd",
                     help="wgrad: the weight gradient dW[n,k] = dy^T.x over m tokens (fp32 out); "
                          "bf16-reference: torch.matmul (hipBLASLt) of the same shape in bf16")
@@ -453,6 +453,13 @@ def bench_one_gemm(torch, nf4, gemm, args):
         b = torch.randn(n, k, device="cuda", generator=g).to(torch.bfloat16)
         o = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
         fn = lambda: torch.matmul(a, b.t(), out=o)
+    elif args.gemm_mode == "swiglu":
+        # hidden = silu(x.Wg^T) * (x.Wu^T), gate and up both of this shape.
+        wu = nf4.quantize_weight(torch.randn(n, k, device="cuda", generator=g) * 0.02,
+                                 double_quant=True)
+        a = torch.randn(m, k, device="cuda", generator=g).to(torch.bfloat16)
+        o = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
+        fn = lambda: gemm.linear_swiglu(a, w, wu, o)
     elif args.gemm_mode == "wgrad":
         a = torch.randn(m, n, device="cuda", generator=g).to(torch.bfloat16)
         b = torch.randn(m, k, device="cuda", generator=g).to(torch.bfloat16)
@@ -463,7 +470,7 @@ def bench_one_gemm(torch, nf4, gemm, args):
         o = torch.empty(m, k, dtype=torch.bfloat16, device="cuda")
         fn = lambda: gemm.linear_dgrad(a, w, o)
     ms = timed(torch, fn, args.steps, args.warmup, name=f"{args.gemm_shape}_{args.gemm_mode}")
-    tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+    tf = (4.0 if args.gemm_mode == "swiglu" else 2.0) * m * n * k / (ms * 1e-3) / 1e12
     print(json.dumps({"gemm_shape": args.gemm_shape, "mode": args.gemm_mode, "m": m, "n": n,
                       "k": k, "ms": round(ms, 4), "tflops": round(tf, 1)}), flush=True)
 
