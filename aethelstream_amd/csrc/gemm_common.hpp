@@ -61,7 +61,22 @@ __device__ __forceinline__ void step_barrier() {
 // tile b runs on XCD b % 8; consecutive logical tiles (same tile_m,
 // neighbouring tile_o) are given to the same XCD so that its resident
 // workgroups share the tile_m operand rows in that XCD's L2.
+//
+// Exception: with 64 output tiles per row block (a 256-CU round covers 4
+// row blocks) XCD pair (x, x + 4) shares one row block per round, each XCD
+// taking 32 of its output tiles: tm = 4r + x % 4, to = 32 (x / 4) + i for
+// round r and slot i.  Both XCDs then read those activation rows at the
+// same time, and the Infinity Cache serves the second; in the XCD-major
+// order one XCD reads them twice, a round apart.  A permutation of
+// [0, tiles_m * 64) for any grid; measured +1.8 % on the 70B down
+// projection (K = 28672, a 470 MB activation), +0.3 % on 70B q.
 __device__ __forceinline__ void map_tile(int b, int tiles_m, int tiles_o, int &tm, int &to) {
+  if (tiles_o == 64 && (tiles_m & 3) == 0) {
+    const int r = b >> 8, x = b & 7, i = (b & 255) >> 3;
+    tm = 4 * r + (x & 3);
+    to = 32 * (x >> 2) + i;
+    return;
+  }
   const int T = tiles_m * tiles_o;
   const int x = b & 7, qq = b >> 3;
   const int base = T >> 3, rem = T & 7;
