@@ -420,3 +420,25 @@ def test_random_shapes_fwd_and_dgrad(case):
     torch.cuda.synchronize()
     assert rel_l2(dx.float().cpu().numpy(), ref.cpu().numpy()) <= TOL_SAME
 
+
+# 64 output tiles per 512-row block switch the tile order to XCD pairs
+# sharing a row block (tiles_m % 4 == 0): ragged rows and a ragged last
+# output tile under that order, forward (n) and input gradient (k).
+@pytest.mark.parametrize("m,wide", [(1800, 8128), (4096, 8192), (2048, 8136)])
+def test_xcd_pair_tile_order(m, wide):
+    print(f"xcd-pair order m={m} wide={wide}", flush=True)
+    k = 256
+    x, _ = _act(m, k, 700 + m)
+    w = _weight(wide, k, 701, True)
+    y = gemm.linear_fwd(x, w)
+    ref = x.float() @ nf4.dequant(w).float().t()
+    torch.cuda.synchronize()
+    assert rel_l2(y.float().cpu().numpy(), ref.cpu().numpy()) <= TOL_SAME
+    n = 128
+    wd = _weight(n, wide - wide % 64, 702, True)
+    dy, _ = _act(m, n, 703)
+    dx = gemm.linear_dgrad(dy, wd)
+    ref = dy.float() @ nf4.dequant(wd).float()
+    torch.cuda.synchronize()
+    assert rel_l2(dx.float().cpu().numpy(), ref.cpu().numpy()) <= TOL_SAME
+
