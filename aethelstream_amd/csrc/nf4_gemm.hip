@@ -1091,6 +1091,37 @@ __global__ void __launch_bounds__(kGemmThreads) nf4_gemm_fixup_kernel(const Grou
       acc[ii][3] += p[ii][3];
     }
   }
+  // Whole-width tile with 16-byte stores: lanes l and l + 32 pair their
+  // halves (as store_tile does) and store 16-byte chunks through a buffer
+  // resource that ends after the wave's last row below M.  70B k alone:
+  // +1.4 % for the whole split launch.
+  if (((reinterpret_cast<uintptr_t>(g.out) & 15) == 0) && ((g.ldo & 7) == 0) &&
+      o0 + kTileO <= g.O && g.ldo < ((int64_t)1 << 23)) {
+    const int64_t left = g.M - m0;
+    const int64_t rows = left <= 0 ? 0 : (left > 128 ? 128 : left);
+    const uint32_t ldo2 = (uint32_t)(g.ldo * 2);
+    const uint16_t *base = rows > 0 ? g.out + m0 * g.ldo + o0 : g.out;
+    const int32_t nrec = rows > 0 ? (int32_t)((rows - 1) * ldo2 + kTileO * 2) : 0;
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void *)base, 0, nrec, kBufferFlags);
+    typedef unsigned int uvec4 __attribute__((ext_vector_type(4)));
+    const int i0 = q * kFixupQuads;  // quads i0..i0+3: one (mt, nt), j = 0..3
+    const uint32_t rowoff = (uint32_t)(32 * (i0 >> 4) + (lane & 31)) * ldo2;
+#pragma unroll
+    for (int jp = 0; jp < 4; jp += 2) {
+      const uint32_t lo0 = pack_bf16x2(acc[jp][0], acc[jp][1]);
+      const uint32_t hi0 = pack_bf16x2(acc[jp][2], acc[jp][3]);
+      const uint32_t lo1 = pack_bf16x2(acc[jp + 1][0], acc[jp + 1][1]);
+      const uint32_t hi1 = pack_bf16x2(acc[jp + 1][2], acc[jp + 1][3]);
+      const auto a = __builtin_amdgcn_permlane32_swap(lo0, lo1, false, false);
+      const auto b = __builtin_amdgcn_permlane32_swap(hi0, hi1, false, false);
+      const uint32_t a0 = a[0], a1 = a[1], b0 = b[0], b1 = b[1];
+      const int c = 4 * ((i0 >> 2) & 3) + jp + (lane >> 5);
+      __builtin_amdgcn_raw_buffer_store_b128((uvec4){a0, b0, a1, b1}, rs,
+                                             (int)(rowoff + 16u * (uint32_t)c), 0, 0);
+    }
+    return;
+  }
 #pragma unroll
   for (int ii = 0; ii < kFixupQuads; ++ii) {
     const int i = q * kFixupQuads + ii;
