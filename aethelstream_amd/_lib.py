@@ -60,6 +60,32 @@ class Nf4sParamInfo(ctypes.Structure):
     ]
 
 
+class Nf4sReadyLayer(ctypes.Structure):
+    """Mirror of ``struct nf4s_ready_layer`` (include/nf4stream.h)."""
+
+    _fields_ = [
+        ("layer_idx", ctypes.c_uint32),
+        ("slab_device_ptr", ctypes.c_void_p),
+        ("bytes", ctypes.c_int64),
+        ("copy_event", ctypes.c_void_p),
+    ]
+
+
+class Nf4sBlobEntry(ctypes.Structure):
+    """Mirror of ``struct nf4s_blob_entry`` (include/nf4stream.h)."""
+
+    _fields_ = [
+        ("packed_off", ctypes.c_int64),
+        ("packed_len", ctypes.c_int64),
+        ("absmax_off", ctypes.c_int64),
+        ("absmax_len", ctypes.c_int64),
+        ("scale_off", ctypes.c_int64),
+        ("scale_len", ctypes.c_int64),
+        ("block_size", ctypes.c_int32),
+        ("dq_group", ctypes.c_int32),
+    ]
+
+
 # Every extern "C" symbol of include/nf4stream.h with its ctypes signature.
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -98,13 +124,20 @@ SIGNATURES = {
                                  ctypes.POINTER(_P)]),
     "nf4s_dbuf_release": (_I32, [_P, _P, _P]),
     "nf4s_stream_wait_event": (_I32, [_P, _P]),
+    "nf4s_take_ready": (_I32, [_P, ctypes.c_uint32, _P, _I64, ctypes.POINTER(Nf4sReadyLayer)]),
+    "nf4s_retire_layer": (_I32, [_P, ctypes.POINTER(Nf4sReadyLayer), _P]),
     "nf4s_loader_open": (_I32, [ctypes.c_char_p, ctypes.POINTER(_P)]),
     "nf4s_loader_close": (_I32, [_P]),
     "nf4s_loader_param_info": (_I32, [_P, ctypes.c_char_p, ctypes.POINTER(Nf4sParamInfo)]),
     "nf4s_loader_load_layer": (_I32, [_P, ctypes.c_uint32, ctypes.POINTER(_P),
                                       ctypes.POINTER(_I64)]),
-    "nf4s_loader_load_param_f16": (_I32, [_P, ctypes.c_char_p, _P, _I64, _P]),
-    "nf4s_loader_load_param_nf4": (_I32, [_P, ctypes.c_char_p, _P, _P, _P, _P]),
+    "nf4s_loader_staging_size": (_I32, [_P, ctypes.c_char_p, ctypes.POINTER(_I64)]),
+    "nf4s_loader_load_param_f16": (_I32, [_P, ctypes.c_char_p, _P, _I64, _P, _I64, _P]),
+    "nf4s_loader_load_param_nf4": (_I32, [_P, ctypes.c_char_p, _P, _I64, _P, _I64, _P, _I64,
+                                          _P]),
+    "nf4s_loader_pack_layer": (_I32, [_P, ctypes.POINTER(ctypes.c_char_p), _I32, _P, _I64,
+                                      ctypes.POINTER(Nf4sBlobEntry), ctypes.POINTER(_I64)]),
+    "nf4s_blob_tensor": (_I32, [ctypes.POINTER(Nf4sBlobEntry), _P, _TP]),
 }
 
 _lib = None

@@ -15,7 +15,10 @@ namespace nf4s {
 // Formats the message returned by nf4s_last_error_message() and returns rc.
 int32_t fail(int32_t rc, const char *fmt, ...);
 
-inline int32_t clear_ok() { return NF4S_OK; }
+// Empties the message of nf4s_last_error_message(); every status-returning
+// entry point calls it first, so the message always belongs to the last call
+// made on this thread and is empty after a successful one.
+void clear_error();
 
 inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
 

@@ -292,10 +292,14 @@ static int32_t wgrad(const uint16_t *dy, const uint16_t *x, int64_t m, int64_t n
   if (!aligned(dy, 16) || !aligned(x, 16))
     return fail(NF4S_ERR_MISALIGNED, "dy and x must be 16-byte aligned");
   if (!aligned(dw, 4)) return fail(NF4S_ERR_MISALIGNED, "dw must be 4-byte aligned");
-  // Lane offsets are 32-bit and a step's offset must stay below 2^31.
+  // Lane offsets are 32-bit and must stay below 2^31 for every row a step
+  // addresses, including the rows past m of the last 64-token step (which
+  // read as zero only while their offsets do not wrap onto real rows).
   const int64_t lim = ((int64_t)1 << 31) - 1;
-  if (m * n * 2 > lim || m * k * 2 > lim)
-    return fail(NF4S_ERR_UNSUPPORTED_SHAPE, "dy or x larger than 2 GiB (m=%lld n=%lld k=%lld)",
+  const int64_t rows = (m + 63) / 64 * 64;
+  if (rows * n * 2 > lim || rows * k * 2 > lim)
+    return fail(NF4S_ERR_UNSUPPORTED_SHAPE,
+                "dy or x larger than 2 GiB with m rounded up to 64 (m=%lld n=%lld k=%lld)",
                 (long long)m, (long long)n, (long long)k);
   WgradArgs g{};
   g.dy = dy;
@@ -332,6 +336,7 @@ extern "C" {
 
 int32_t nf4s_gemm_wgrad(const void *dy, const void *x, int64_t m, int64_t n, int64_t k,
                         float *dw, int32_t accumulate, void *stream) {
+  clear_error();
   return wgrad(static_cast<const uint16_t *>(dy), static_cast<const uint16_t *>(x), m, n, k, dw,
                accumulate, as_stream(stream));
 }

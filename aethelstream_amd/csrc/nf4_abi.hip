@@ -13,6 +13,8 @@ int32_t fail(int32_t rc, const char *fmt, ...) {
   return rc;
 }
 
+void clear_error() { g_msg[0] = '\0'; }
+
 int32_t check_launch(const char *what) {
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(NF4S_ERR_HIP, "%s: %s", what, hipGetErrorString(e));

@@ -419,6 +419,7 @@ extern "C" {
 
 int32_t nf4s_quantize(const float *x, int64_t n, int32_t block_size, uint8_t *packed,
                       float *absmax, void *stream) {
+  clear_error();
   if (n < 0) return fail(NF4S_ERR_INVALID_ARGUMENT, "negative element count");
   if (block_size <= 0) return fail(NF4S_ERR_INVALID_ARGUMENT, "block_size must be positive");
   if (n == 0) return NF4S_OK;
@@ -444,6 +445,7 @@ int32_t nf4s_quantize(const float *x, int64_t n, int32_t block_size, uint8_t *pa
 
 int32_t nf4s_quantize_bf16(const uint16_t *x, int64_t n, int32_t block_size, uint8_t *packed,
                            float *absmax, void *stream) {
+  clear_error();
   if (n < 0) return fail(NF4S_ERR_INVALID_ARGUMENT, "negative element count");
   if (block_size != 64)
     return fail(NF4S_ERR_UNSUPPORTED_SHAPE, "bf16 quantize needs block_size 64, got %d",
@@ -459,17 +461,20 @@ int32_t nf4s_quantize_bf16(const uint16_t *x, int64_t n, int32_t block_size, uin
 
 int32_t nf4s_quantize_dq(const float *x, int64_t n, int32_t block_size, int32_t group,
                          uint8_t *packed, uint8_t *absmax_q, float *absmax_scale, void *stream) {
+  clear_error();
   return quantize_dq<float>(x, n, block_size, group, packed, absmax_q, absmax_scale, stream);
 }
 
 int32_t nf4s_quantize_dq_bf16(const uint16_t *x, int64_t n, int32_t block_size, int32_t group,
                               uint8_t *packed, uint8_t *absmax_q, float *absmax_scale,
                               void *stream) {
+  clear_error();
   return quantize_dq<uint16_t>(x, n, block_size, group, packed, absmax_q, absmax_scale, stream);
 }
 
 int32_t nf4s_dq_encode(const float *absmax, int64_t nblocks, int32_t group, uint8_t *q,
                        float *scale, void *stream) {
+  clear_error();
   if (nblocks < 0 || group <= 0)
     return fail(NF4S_ERR_INVALID_ARGUMENT, "nblocks must be >= 0 and group > 0");
   if (nblocks == 0) return NF4S_OK;
@@ -483,12 +488,14 @@ int32_t nf4s_dq_encode(const float *absmax, int64_t nblocks, int32_t group, uint
 }
 
 int32_t nf4s_dequant_f16(const nf4s_tensor *t, int64_t n, uint16_t *out, void *stream) {
+  clear_error();
   if (t == nullptr) return fail(NF4S_ERR_INVALID_ARGUMENT, "tensor descriptor is NULL");
   uint16_t *outs[1] = {out};
   return dequant_batch<true>(t, &n, outs, 1, as_stream(stream));
 }
 
 int32_t nf4s_dequant_bf16(const nf4s_tensor *t, int64_t n, uint16_t *out, void *stream) {
+  clear_error();
   if (t == nullptr) return fail(NF4S_ERR_INVALID_ARGUMENT, "tensor descriptor is NULL");
   uint16_t *outs[1] = {out};
   return dequant_batch<false>(t, &n, outs, 1, as_stream(stream));
@@ -496,6 +503,7 @@ int32_t nf4s_dequant_bf16(const nf4s_tensor *t, int64_t n, uint16_t *out, void *
 
 int32_t nf4s_dequant_batch_bf16(const nf4s_tensor *ts, const int64_t *ns, uint16_t *const *outs,
                                 int32_t count, void *stream) {
+  clear_error();
   return dequant_batch<false>(ts, ns, outs, count, as_stream(stream));
 }
 

@@ -1535,6 +1535,30 @@ static int32_t gemm_dgrad_groups(const uint16_t *const *dys, const nf4s_tensor *
   return dq ? launch_dgrad<DgradProducer<true>>(ga, s) : launch_dgrad<DgradProducer<false>>(ga, s);
 }
 
+// Workspace bytes the split-K forward over these weights needs (0: no split
+// would help, or a shape the GEMM itself rejects, which the GEMM reports).
+// Weights of one kind share a launch and a mixed set runs one launch per
+// kind, so this is the largest plan over every subset of the weights and
+// both producers' step multiples: enough for any partition into launches.
+static int64_t fwd_workspace_bytes(const int64_t *ns, int32_t count, int64_t m, int64_t k) {
+  if (m <= 0 || k <= 0 || k % 64 != 0) return 0;
+  for (int32_t i = 0; i < count; ++i)
+    if (ns[i] <= 0) return 0;
+  const int64_t tiles_m = (m + kTileM - 1) / kTileM;
+  int64_t best = 0;
+  for (uint32_t set = 1; set < (1u << count); ++set) {
+    int64_t tiles_o = 0;
+    for (int32_t i = 0; i < count; ++i)
+      if (set & (1u << i)) tiles_o += (ns[i] + kTileO - 1) / kTileO;
+    const int64_t T = tiles_m * tiles_o;
+    for (int unroll : {2, 4}) {
+      const int64_t b = split_bytes(split_plan(T, k / kStep, unroll));
+      if (b > best) best = b;
+    }
+  }
+  return best;
+}
+
 }  // namespace nf4s
 
 using namespace nf4s;
@@ -1543,6 +1567,7 @@ extern "C" {
 
 int32_t nf4s_gemm_fwd(const uint16_t *x, const nf4s_tensor *w, int64_t m, int64_t n, int64_t k,
                       uint16_t *y, void *stream) {
+  clear_error();
   if (w == nullptr) return fail(NF4S_ERR_INVALID_ARGUMENT, "weight descriptor is NULL");
   uint16_t *ys[1] = {y};
   return gemm_fwd_groups(x, w, &n, ys, 1, m, k, as_stream(stream));
@@ -1550,6 +1575,7 @@ int32_t nf4s_gemm_fwd(const uint16_t *x, const nf4s_tensor *w, int64_t m, int64_
 
 int32_t nf4s_gemm_dgrad(const uint16_t *dy, const nf4s_tensor *w, int64_t m, int64_t n,
                         int64_t k, uint16_t *dx, void *stream) {
+  clear_error();
   if (w == nullptr) return fail(NF4S_ERR_INVALID_ARGUMENT, "weight descriptor is NULL");
   const uint16_t *dys[1] = {dy};
   return gemm_dgrad_groups(dys, w, &n, 1, m, k, dx, as_stream(stream));
@@ -1558,12 +1584,14 @@ int32_t nf4s_gemm_dgrad(const uint16_t *dy, const nf4s_tensor *w, int64_t m, int
 int32_t nf4s_gemm_fwd_grouped(const uint16_t *x, const nf4s_tensor *ws, const int64_t *ns,
                               uint16_t *const *ys, int32_t count, int64_t m, int64_t k,
                               void *stream) {
+  clear_error();
   return gemm_fwd_groups(x, ws, ns, ys, count, m, k, as_stream(stream));
 }
 
 int32_t nf4s_gemm_fwd_grouped_ws(const uint16_t *x, const nf4s_tensor *ws, const int64_t *ns,
                                  uint16_t *const *ys, int32_t count, int64_t m, int64_t k,
                                  void *workspace, int64_t workspace_bytes, void *stream) {
+  clear_error();
   if (workspace_bytes < 0)
     return fail(NF4S_ERR_INVALID_ARGUMENT, "negative workspace size %lld",
                 (long long)workspace_bytes);
@@ -1575,38 +1603,25 @@ int32_t nf4s_gemm_fwd_grouped_ws(const uint16_t *x, const nf4s_tensor *ws, const
 
 int32_t nf4s_gemm_fwd_workspace_size(const int64_t *ns, int32_t count, int64_t m, int64_t k,
                                      int64_t *bytes) {
+  clear_error();
   if (bytes == nullptr) return fail(NF4S_ERR_INVALID_ARGUMENT, "bytes is NULL");
   *bytes = 0;
   if (count <= 0 || count > kMaxGroups || ns == nullptr)
     return fail(NF4S_ERR_INVALID_ARGUMENT, "count must be 1..%d with sizes", kMaxGroups);
-  // Shapes the GEMM itself rejects need no workspace; the GEMM call reports
-  // them with its own message.
-  if (m <= 0 || k <= 0 || k % 64 != 0) return NF4S_OK;
-  int64_t tiles_o = 0;
-  for (int32_t i = 0; i < count; ++i) {
-    if (ns[i] <= 0) return NF4S_OK;
-    tiles_o += (ns[i] + kTileO - 1) / kTileO;
-  }
-  // The plan of one launch over all the weights (weights of one kind), the
-  // larger of the two producers' step multiples.  A mixed set runs one
-  // launch per kind; a launch whose plan needs more than the workspace
-  // given runs without a split.
-  const int64_t T = (m + kTileM - 1) / kTileM * tiles_o;
-  if (T == 0) return NF4S_OK;
-  const int64_t a = split_bytes(split_plan(T, k / kStep, 2));
-  const int64_t b = split_bytes(split_plan(T, k / kStep, 4));
-  *bytes = a > b ? a : b;
+  *bytes = fwd_workspace_bytes(ns, count, m, k);
   return NF4S_OK;
 }
 
 int32_t nf4s_gemm_fwd_swiglu(const uint16_t *x, const nf4s_tensor *w_gate,
                              const nf4s_tensor *w_up, int64_t m, int64_t ff, int64_t k,
                              uint16_t *hidden, void *stream) {
+  clear_error();
   return gemm_swiglu(x, w_gate, w_up, m, ff, k, hidden, as_stream(stream));
 }
 
 int32_t nf4s_gemm_dgrad_sum(const uint16_t *const *dys, const nf4s_tensor *ws, const int64_t *ns,
                             int32_t count, int64_t m, int64_t k, uint16_t *dx, void *stream) {
+  clear_error();
   return gemm_dgrad_groups(dys, ws, ns, count, m, k, dx, as_stream(stream));
 }
 

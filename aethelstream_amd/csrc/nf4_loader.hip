@@ -229,8 +229,6 @@ struct nf4s_loader {
   std::map<std::string, nf4s::TensorInfo> index;
   std::map<std::string, std::string> registry;
   std::map<std::string, std::unique_ptr<nf4s::MappedFile>> mmap_cache;
-  void *staging = nullptr;  // device bytes for packed + absmax payloads
-  int64_t staging_bytes = 0;
 };
 
 namespace nf4s {
@@ -262,46 +260,69 @@ static bool read_file(const std::string &path, std::string &out, int &err) {
   return true;
 }
 
-static bool get_int(const Json *j, int64_t &v) {
-  if (j == nullptr || j->kind != Json::Num || !j->is_int) return false;
-  v = j->inum;
+// A usize field of TensorInfo (index.rs:7-34).  Absent or null leaves
+// `present` false (Option::None); anything but a non-negative integer is the
+// error serde reports for a usize (index.rs:282-284 maps it to Json).
+static bool get_usize(const Json &j, const char *key, int64_t &v, bool &present,
+                      std::string &err) {
+  present = false;
+  const Json *f = j.get(key);
+  if (f == nullptr || f->kind == Json::Null) return true;
+  if (f->kind != Json::Num || !f->is_int) {
+    err = std::string("invalid type for field `") + key + "`, expected usize";
+    return false;
+  }
+  if (f->inum < 0) {
+    err = "invalid value: integer `" + std::to_string(f->inum) + "`, expected usize";
+    return false;
+  }
+  v = f->inum;
+  present = true;
   return true;
 }
 
-// Deserializes one TensorInfo; missing required fields are a JSON error, as
-// serde would report them (index.rs:282-284).
+static bool require_usize(const Json &j, const char *key, int64_t &v, std::string &err) {
+  bool present = false;
+  if (!get_usize(j, key, v, present, err)) return false;
+  if (!present) err = std::string("missing field `") + key + "`";
+  return present;
+}
+
+// Deserializes one TensorInfo; missing required fields and negative sizes
+// are a JSON error, as serde would report them (index.rs:282-284).
 static bool parse_info(const Json &j, TensorInfo &t, std::string &err) {
   if (j.kind != Json::Obj) { err = "tensor entry is not an object"; return false; }
   const Json *fp = j.get("file_path"), *dt = j.get("dtype"), *pr = j.get("precision"),
              *sh = j.get("shape");
   if (fp == nullptr || fp->kind != Json::Str) { err = "missing field `file_path`"; return false; }
-  if (!get_int(j.get("byte_offset"), t.byte_offset) || t.byte_offset < 0) {
-    err = "missing field `byte_offset`";
-    return false;
-  }
-  if (!get_int(j.get("byte_length"), t.byte_length) || t.byte_length < 0) {
-    err = "missing field `byte_length`";
-    return false;
-  }
+  if (!require_usize(j, "byte_offset", t.byte_offset, err)) return false;
+  if (!require_usize(j, "byte_length", t.byte_length, err)) return false;
   if (sh == nullptr || sh->kind != Json::Arr) { err = "missing field `shape`"; return false; }
   for (const Json &d : sh->arr) {
-    int64_t v;
-    if (!get_int(&d, v) || v < 0) { err = "invalid shape entry"; return false; }
-    t.shape.push_back(v);
+    if (d.kind != Json::Num || !d.is_int) { err = "invalid shape entry, expected usize"; return false; }
+    if (d.inum < 0) {
+      err = "invalid value: integer `" + std::to_string(d.inum) + "`, expected usize";
+      return false;
+    }
+    t.shape.push_back(d.inum);
   }
   if (dt == nullptr || dt->kind != Json::Str) { err = "missing field `dtype`"; return false; }
   if (pr == nullptr || pr->kind != Json::Str) { err = "missing field `precision`"; return false; }
   t.file_path = fp->str;
   t.dtype = dt->str;
   t.precision = pr->str;
-  t.has_absmax_offset = get_int(j.get("nf4_absmax_offset"), t.absmax_offset);
-  t.has_absmax_length = get_int(j.get("nf4_absmax_length"), t.absmax_length);
-  t.has_block_size = get_int(j.get("nf4_block_size"), t.block_size);
-  t.dq = get_int(j.get("nf4_absmax_q_offset"), t.q_offset) &&
-         get_int(j.get("nf4_absmax_q_length"), t.q_length) &&
-         get_int(j.get("nf4_absmax_scale_offset"), t.scale_offset) &&
-         get_int(j.get("nf4_absmax_scale_length"), t.scale_length) &&
-         get_int(j.get("nf4_dq_group"), t.dq_group);
+  if (!get_usize(j, "nf4_absmax_offset", t.absmax_offset, t.has_absmax_offset, err) ||
+      !get_usize(j, "nf4_absmax_length", t.absmax_length, t.has_absmax_length, err) ||
+      !get_usize(j, "nf4_block_size", t.block_size, t.has_block_size, err))
+    return false;
+  bool dq[5];
+  if (!get_usize(j, "nf4_absmax_q_offset", t.q_offset, dq[0], err) ||
+      !get_usize(j, "nf4_absmax_q_length", t.q_length, dq[1], err) ||
+      !get_usize(j, "nf4_absmax_scale_offset", t.scale_offset, dq[2], err) ||
+      !get_usize(j, "nf4_absmax_scale_length", t.scale_length, dq[3], err) ||
+      !get_usize(j, "nf4_dq_group", t.dq_group, dq[4], err))
+    return false;
+  t.dq = dq[0] && dq[1] && dq[2] && dq[3] && dq[4];
   return true;
 }
 
@@ -363,20 +384,25 @@ static int32_t lookup(nf4s_loader *L, const char *name, const TensorInfo **out) 
 
 static bool is_nf4(const TensorInfo &t) { return t.precision == "nf4"; }
 
+// off + len > size without the wrap of the sum (parse_info keeps both >= 0).
+static bool beyond(int64_t off, int64_t len, uint64_t size) {
+  return (uint64_t)off > size || (uint64_t)len > size - (uint64_t)off;
+}
+
 // The NF4 checks of loader.rs:93-151 (bounds, required fields, alignment),
 // extended to the double-quant fields.
 static int32_t check_nf4(const std::string &name, const TensorInfo &t, const MappedFile &m) {
   const uint64_t sz = m.size;
-  if ((uint64_t)t.byte_offset + (uint64_t)t.byte_length > sz)
+  if (beyond(t.byte_offset, t.byte_length, sz))
     return malformed(name, "packed data out of bounds: offset %lld + length %lld > mmap %llu",
                      (long long)t.byte_offset, (long long)t.byte_length, (unsigned long long)sz);
   if (t.dq) {
     if (t.dq_group <= 0 || (t.dq_group & (t.dq_group - 1)) != 0)
       return malformed(name, "nf4_dq_group must be a power of two");
-    if ((uint64_t)t.q_offset + (uint64_t)t.q_length > sz)
+    if (beyond(t.q_offset, t.q_length, sz))
       return malformed(name, "absmax codes out of bounds: offset %lld + length %lld > mmap %llu",
                        (long long)t.q_offset, (long long)t.q_length, (unsigned long long)sz);
-    if ((uint64_t)t.scale_offset + (uint64_t)t.scale_length > sz)
+    if (beyond(t.scale_offset, t.scale_length, sz))
       return malformed(name, "absmax scales out of bounds: offset %lld + length %lld > mmap %llu",
                        (long long)t.scale_offset, (long long)t.scale_length,
                        (unsigned long long)sz);
@@ -389,7 +415,7 @@ static int32_t check_nf4(const std::string &name, const TensorInfo &t, const Map
   if (!t.has_absmax_offset) return malformed(name, "missing nf4_absmax_offset");
   if (!t.has_absmax_length) return malformed(name, "missing nf4_absmax_length");
   if (!t.has_block_size) return malformed(name, "missing nf4_block_size");
-  if ((uint64_t)t.absmax_offset + (uint64_t)t.absmax_length > sz)
+  if (beyond(t.absmax_offset, t.absmax_length, sz))
     return malformed(name, "absmax data out of bounds: offset %lld + length %lld > mmap %llu",
                      (long long)t.absmax_offset, (long long)t.absmax_length,
                      (unsigned long long)sz);
@@ -398,22 +424,27 @@ static int32_t check_nf4(const std::string &name, const TensorInfo &t, const Map
   return NF4S_OK;
 }
 
-static int32_t ensure_staging(nf4s_loader *L, int64_t bytes) {
-  if (bytes <= L->staging_bytes) return NF4S_OK;
-  if (L->staging != nullptr) {
-    // A previous call's kernels may still read the old buffer.
-    (void)hipDeviceSynchronize();
-    (void)hipFree(L->staging);
-    L->staging = nullptr;
-    L->staging_bytes = 0;
-  }
-  const hipError_t e = hipMalloc(&L->staging, (size_t)bytes);
-  if (e != hipSuccess) return fail(NF4S_ERR_HIP, "staging hipMalloc: %s", hipGetErrorString(e));
-  L->staging_bytes = bytes;
-  return NF4S_OK;
-}
+// Bytes of the fp32 parts that are read: the reference views an absmax
+// byte range as floor(len / 4) floats (loader.rs:158-161).
+static int64_t f32_bytes(int64_t len) { return len / 4 * 4; }
 
 static int64_t round_up(int64_t x) { return (x + 255) / 256 * 256; }
+
+// Staging layout of one NF4 parameter: packed bytes, then the absmax part,
+// then the double-quant scales, each at a 256-byte boundary.
+struct Staging {
+  int64_t am_off, sc_off, bytes, am_bytes, sc_bytes;
+};
+
+static Staging staging_of(const TensorInfo &t) {
+  Staging g;
+  g.am_bytes = t.dq ? t.q_length : f32_bytes(t.absmax_length);
+  g.sc_bytes = t.dq ? f32_bytes(t.scale_length) : 0;
+  g.am_off = round_up(t.byte_length);
+  g.sc_off = g.am_off + round_up(g.am_bytes);
+  g.bytes = g.sc_off + round_up(g.sc_bytes);
+  return g;
+}
 
 }  // namespace nf4s
 
@@ -423,6 +454,7 @@ extern "C" {
 
 // ShardLoader::new (loader.rs:44-50) -> IndexStore::load (index.rs:279-295).
 int32_t nf4s_loader_open(const char *model_dir, nf4s_loader **out) {
+  clear_error();
   if (model_dir == nullptr || out == nullptr)
     return fail(NF4S_ERR_INVALID_ARGUMENT, "bad loader_open args");
   *out = nullptr;
@@ -461,16 +493,13 @@ int32_t nf4s_loader_open(const char *model_dir, nf4s_loader **out) {
 }
 
 int32_t nf4s_loader_close(nf4s_loader *L) {
-  if (L == nullptr) return NF4S_OK;
-  if (L->staging != nullptr) {
-    (void)hipDeviceSynchronize();
-    (void)hipFree(L->staging);
-  }
+  clear_error();
   delete L;
   return NF4S_OK;
 }
 
 int32_t nf4s_loader_param_info(nf4s_loader *L, const char *name, nf4s_param_info *out) {
+  clear_error();
   if (L == nullptr || out == nullptr) return fail(NF4S_ERR_INVALID_ARGUMENT, "bad args");
   const TensorInfo *t;
   int32_t rc = lookup(L, name, &t);
@@ -505,6 +534,7 @@ int32_t nf4s_loader_param_info(nf4s_loader *L, const char *name, nf4s_param_info
 // Returns a pointer into the loader's read-only mapping, valid until close.
 int32_t nf4s_loader_load_layer(nf4s_loader *L, uint32_t layer, const uint8_t **data,
                                int64_t *len) {
+  clear_error();
   if (L == nullptr || data == nullptr || len == nullptr)
     return fail(NF4S_ERR_INVALID_ARGUMENT, "bad args");
   auto it = L->registry.find(std::to_string(layer));
@@ -518,13 +548,28 @@ int32_t nf4s_loader_load_layer(nf4s_loader *L, uint32_t layer, const uint8_t **d
   return NF4S_OK;
 }
 
+// Device staging bytes nf4s_loader_load_param_f16 needs for `name` (0 for an
+// fp16 entry, which is copied straight into the output).
+int32_t nf4s_loader_staging_size(nf4s_loader *L, const char *name, int64_t *bytes) {
+  clear_error();
+  if (L == nullptr || bytes == nullptr) return fail(NF4S_ERR_INVALID_ARGUMENT, "bad args");
+  *bytes = 0;
+  const TensorInfo *t;
+  const int32_t rc = lookup(L, name, &t);
+  if (rc != NF4S_OK) return rc;
+  if (is_nf4(*t)) *bytes = staging_of(*t).bytes;
+  return NF4S_OK;
+}
+
 // ShardLoader::load_param (loader.rs:78-206) into a device f16 buffer of
-// out_len elements: NF4 entries are dequantized on the device
-// (dequant_nf4_alloc semantics: 2 * packed bytes elements); fp16 entries are
-// copied (loader.rs:179-198).  Uses the loader's device staging buffer: one
-// stream at a time per loader (the reference's loader needs &mut self).
+// out_len elements: NF4 entries are copied into the caller's device staging
+// buffer and dequantized on the device (dequant_nf4_alloc semantics: 2 *
+// packed bytes elements); fp16 entries are copied (loader.rs:179-198).
+// Allocates nothing and never synchronizes the device.
 int32_t nf4s_loader_load_param_f16(nf4s_loader *L, const char *name, uint16_t *out,
-                                   int64_t out_len, void *stream) {
+                                   int64_t out_len, void *staging, int64_t staging_bytes,
+                                   void *stream) {
+  clear_error();
   if (L == nullptr || out == nullptr) return fail(NF4S_ERR_INVALID_ARGUMENT, "bad args");
   const TensorInfo *t;
   int32_t rc = lookup(L, name, &t);
@@ -534,11 +579,11 @@ int32_t nf4s_loader_load_param_f16(nf4s_loader *L, const char *name, uint16_t *o
   if (rc != NF4S_OK) return rc;
   hipStream_t s = as_stream(stream);
   if (!is_nf4(*t)) {
-    if ((uint64_t)t->byte_offset + (uint64_t)t->byte_length > m->size)
+    if (beyond(t->byte_offset, t->byte_length, m->size))
       return malformed(name, "tensor data out of bounds: offset %lld + length %lld > mmap %llu",
                        (long long)t->byte_offset, (long long)t->byte_length,
                        (unsigned long long)m->size);
-    if (out_len * 2 < t->byte_length)
+    if (out_len < 0 || out_len * 2 < t->byte_length)
       return fail(NF4S_ERR_INVALID_ARGUMENT, "output holds %lld elements, need %lld",
                   (long long)out_len, (long long)(t->byte_length / 2));
     const hipError_t e = hipMemcpyAsync(out, m->data + t->byte_offset, (size_t)t->byte_length,
@@ -552,20 +597,19 @@ int32_t nf4s_loader_load_param_f16(nf4s_loader *L, const char *name, uint16_t *o
   if (out_len < n)
     return fail(NF4S_ERR_INVALID_ARGUMENT, "output holds %lld elements, need %lld",
                 (long long)out_len, (long long)n);
-  const int64_t am_bytes = t->dq ? t->q_length : t->absmax_length;
-  const int64_t sc_bytes = t->dq ? t->scale_length : 0;
-  const int64_t o_am = round_up(t->byte_length);
-  const int64_t o_sc = o_am + round_up(am_bytes);
-  rc = ensure_staging(L, o_sc + round_up(sc_bytes));
-  if (rc != NF4S_OK) return rc;
-  uint8_t *st = static_cast<uint8_t *>(L->staging);
+  const Staging g = staging_of(*t);
+  if (staging == nullptr || staging_bytes < g.bytes)
+    return fail(NF4S_ERR_INVALID_ARGUMENT, "staging holds %lld bytes, need %lld",
+                (long long)(staging == nullptr ? 0 : staging_bytes), (long long)g.bytes);
+  if (!aligned(staging, 16)) return fail(NF4S_ERR_MISALIGNED, "staging must be 16-byte aligned");
+  uint8_t *st = static_cast<uint8_t *>(staging);
   hipError_t e = hipMemcpyAsync(st, m->data + t->byte_offset, (size_t)t->byte_length,
                                 hipMemcpyHostToDevice, s);
-  if (e == hipSuccess && am_bytes > 0)
-    e = hipMemcpyAsync(st + o_am, m->data + (t->dq ? t->q_offset : t->absmax_offset),
-                       (size_t)am_bytes, hipMemcpyHostToDevice, s);
-  if (e == hipSuccess && sc_bytes > 0)
-    e = hipMemcpyAsync(st + o_sc, m->data + t->scale_offset, (size_t)sc_bytes,
+  if (e == hipSuccess && g.am_bytes > 0)
+    e = hipMemcpyAsync(st + g.am_off, m->data + (t->dq ? t->q_offset : t->absmax_offset),
+                       (size_t)g.am_bytes, hipMemcpyHostToDevice, s);
+  if (e == hipSuccess && g.sc_bytes > 0)
+    e = hipMemcpyAsync(st + g.sc_off, m->data + t->scale_offset, (size_t)g.sc_bytes,
                        hipMemcpyHostToDevice, s);
   if (e != hipSuccess) return fail(NF4S_ERR_HIP, "hipMemcpyAsync: %s", hipGetErrorString(e));
   nf4s_tensor d{};
@@ -573,24 +617,28 @@ int32_t nf4s_loader_load_param_f16(nf4s_loader *L, const char *name, uint16_t *o
   d.packed_len = t->byte_length;
   d.block_size = (int32_t)t->block_size;
   if (t->dq) {
-    d.absmax_q = st + o_am;
-    d.absmax_scale = reinterpret_cast<const float *>(st + o_sc);
+    d.absmax_q = st + g.am_off;
+    d.absmax_scale = reinterpret_cast<const float *>(st + g.sc_off);
     d.absmax_len = t->q_length;
     d.scale_len = t->scale_length / 4;
     d.dq_group = (int32_t)t->dq_group;
   } else {
-    d.absmax = reinterpret_cast<const float *>(st + o_am);
+    d.absmax = reinterpret_cast<const float *>(st + g.am_off);
     d.absmax_len = t->absmax_length / 4;  // loader.rs:160
   }
   // dequant_nf4_alloc (nf4.rs:98-107) -> dequant_nf4_into checks (nf4.rs:46-57)
   return nf4s_dequant_f16(&d, n, out, stream);
 }
 
-// The raw NF4 payload of a parameter copied into caller device buffers (the
-// device-resident weight provider keeps NF4 on the device instead of f32).
-// Buffers may be NULL when the entry has no such part.
+// The raw NF4 payload of a parameter copied into caller device buffers of the
+// given byte capacities (the device-resident weight provider keeps NF4 on the
+// device instead of f32).  The fp32 parts copy floor(length / 4) floats, as
+// many as the reference reads (loader.rs:158-161); `scale` may be NULL for
+// an entry without double-quant.
 int32_t nf4s_loader_load_param_nf4(nf4s_loader *L, const char *name, uint8_t *packed,
-                                   void *absmax_or_q, float *scale, void *stream) {
+                                   int64_t packed_bytes, void *absmax_or_q, int64_t absmax_bytes,
+                                   float *scale, int64_t scale_bytes, void *stream) {
+  clear_error();
   if (L == nullptr) return fail(NF4S_ERR_INVALID_ARGUMENT, "bad args");
   const TensorInfo *t;
   int32_t rc = lookup(L, name, &t);
@@ -601,19 +649,131 @@ int32_t nf4s_loader_load_param_nf4(nf4s_loader *L, const char *name, uint8_t *pa
   if (rc != NF4S_OK) return rc;
   rc = check_nf4(name, *t, *m);
   if (rc != NF4S_OK) return rc;
+  const Staging g = staging_of(*t);
   if (packed == nullptr || absmax_or_q == nullptr || (t->dq && scale == nullptr))
     return fail(NF4S_ERR_INVALID_ARGUMENT, "NULL destination buffer");
+  if (packed_bytes < t->byte_length || absmax_bytes < g.am_bytes || scale_bytes < g.sc_bytes)
+    return fail(NF4S_ERR_INVALID_ARGUMENT,
+                "destination too small: packed %lld < %lld, absmax %lld < %lld or scale %lld < %lld",
+                (long long)packed_bytes, (long long)t->byte_length, (long long)absmax_bytes,
+                (long long)g.am_bytes, (long long)scale_bytes, (long long)g.sc_bytes);
   hipStream_t s = as_stream(stream);
   hipError_t e = hipMemcpyAsync(packed, m->data + t->byte_offset, (size_t)t->byte_length,
                                 hipMemcpyHostToDevice, s);
   const int64_t am_off = t->dq ? t->q_offset : t->absmax_offset;
-  const int64_t am_len = t->dq ? t->q_length : t->absmax_length;
-  if (e == hipSuccess && am_len > 0)
-    e = hipMemcpyAsync(absmax_or_q, m->data + am_off, (size_t)am_len, hipMemcpyHostToDevice, s);
-  if (e == hipSuccess && t->dq && t->scale_length > 0)
-    e = hipMemcpyAsync(scale, m->data + t->scale_offset, (size_t)t->scale_length,
+  if (e == hipSuccess && g.am_bytes > 0)
+    e = hipMemcpyAsync(absmax_or_q, m->data + am_off, (size_t)g.am_bytes, hipMemcpyHostToDevice,
+                       s);
+  if (e == hipSuccess && g.sc_bytes > 0)
+    e = hipMemcpyAsync(scale, m->data + t->scale_offset, (size_t)g.sc_bytes,
                        hipMemcpyHostToDevice, s);
   if (e != hipSuccess) return fail(NF4S_ERR_HIP, "hipMemcpyAsync: %s", hipGetErrorString(e));
+  return NF4S_OK;
+}
+
+}  // extern "C"
+
+namespace nf4s {
+
+// Placement of one NF4 parameter's parts in a layer blob: packed bytes, the
+// absmax part (fp32 or uint8 codes), the double-quant scales, each at the
+// next 256-byte boundary after the previous part.
+static int32_t place_entry(nf4s_loader *L, const char *name, int64_t at, nf4s_blob_entry &e,
+                           const TensorInfo **info, const MappedFile **map, int64_t *end) {
+  const TensorInfo *t;
+  int32_t rc = lookup(L, name, &t);
+  if (rc != NF4S_OK) return rc;
+  if (!is_nf4(*t)) return malformed(name, "precision is %s, not nf4", t->precision.c_str());
+  const MappedFile *m;
+  rc = get_mmap(L, t->file_path, &m);
+  if (rc != NF4S_OK) return rc;
+  rc = check_nf4(name, *t, *m);
+  if (rc != NF4S_OK) return rc;
+  if (t->block_size <= 0 || t->block_size > 0x7fffffff || t->dq_group > 0x7fffffff)
+    return malformed(name, "nf4_block_size %lld or nf4_dq_group %lld out of range",
+                     (long long)t->block_size, (long long)t->dq_group);
+  const Staging g = staging_of(*t);
+  e = nf4s_blob_entry{};
+  e.packed_off = at;
+  e.packed_len = t->byte_length;
+  e.absmax_off = at + g.am_off;
+  e.absmax_len = t->dq ? t->q_length : g.am_bytes / 4;
+  e.scale_off = t->dq ? at + g.sc_off : 0;
+  e.scale_len = g.sc_bytes / 4;
+  e.block_size = (int32_t)t->block_size;
+  e.dq_group = t->dq ? (int32_t)t->dq_group : 0;
+  *info = t;
+  *map = m;
+  *end = at + g.bytes;
+  return NF4S_OK;
+}
+
+}  // namespace nf4s
+
+extern "C" {
+
+// The bytes a FlowCast pinned slot holds for one layer (ready.rs:27-30):
+// the raw NF4 payloads of `count` parameters packed into one host blob, so
+// that one asynchronous H2D copy moves the layer.
+int32_t nf4s_loader_pack_layer(nf4s_loader *L, const char *const *names, int32_t count,
+                               void *dst, int64_t dst_bytes, nf4s_blob_entry *entries,
+                               int64_t *bytes) {
+  clear_error();
+  if (L == nullptr || names == nullptr || entries == nullptr || bytes == nullptr || count < 0)
+    return fail(NF4S_ERR_INVALID_ARGUMENT, "bad pack_layer args");
+  *bytes = 0;
+  int64_t at = 0;
+  for (int32_t i = 0; i < count; ++i) {
+    const TensorInfo *t;
+    const MappedFile *m;
+    int64_t end = 0;
+    const int32_t rc = place_entry(L, names[i], at, entries[i], &t, &m, &end);
+    if (rc != NF4S_OK) return rc;
+    at = end;
+  }
+  *bytes = at;
+  if (dst == nullptr) return NF4S_OK;
+  if (dst_bytes < at)
+    return fail(NF4S_ERR_INVALID_ARGUMENT, "blob holds %lld bytes, need %lld",
+                (long long)dst_bytes, (long long)at);
+  uint8_t *out = static_cast<uint8_t *>(dst);
+  memset(out, 0, (size_t)at);  // alignment gaps
+  for (int32_t i = 0; i < count; ++i) {
+    const TensorInfo *t;
+    const MappedFile *m;
+    int64_t end = 0;
+    nf4s_blob_entry e;
+    const int32_t rc = place_entry(L, names[i], entries[i].packed_off, e, &t, &m, &end);
+    if (rc != NF4S_OK) return rc;
+    memcpy(out + e.packed_off, m->data + t->byte_offset, (size_t)e.packed_len);
+    const int64_t am_bytes = t->dq ? e.absmax_len : 4 * e.absmax_len;
+    memcpy(out + e.absmax_off, m->data + (t->dq ? t->q_offset : t->absmax_offset),
+           (size_t)am_bytes);
+    if (e.scale_len > 0)
+      memcpy(out + e.scale_off, m->data + t->scale_offset, (size_t)(4 * e.scale_len));
+  }
+  return NF4S_OK;
+}
+
+// Descriptor of blob entry `e` inside a copy of the blob at `base`.
+int32_t nf4s_blob_tensor(const nf4s_blob_entry *e, const void *base, nf4s_tensor *out) {
+  clear_error();
+  if (e == nullptr || base == nullptr || out == nullptr)
+    return fail(NF4S_ERR_INVALID_ARGUMENT, "bad blob_tensor args");
+  const uint8_t *b = static_cast<const uint8_t *>(base);
+  *out = nf4s_tensor{};
+  out->packed = b + e->packed_off;
+  out->packed_len = e->packed_len;
+  if (e->dq_group > 0) {
+    out->absmax_q = b + e->absmax_off;
+    out->absmax_scale = reinterpret_cast<const float *>(b + e->scale_off);
+    out->scale_len = e->scale_len;
+  } else {
+    out->absmax = reinterpret_cast<const float *>(b + e->absmax_off);
+  }
+  out->absmax_len = e->absmax_len;
+  out->block_size = e->block_size;
+  out->dq_group = e->dq_group;
   return NF4S_OK;
 }
 

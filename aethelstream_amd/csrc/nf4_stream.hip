@@ -23,6 +23,8 @@ struct nf4s_dbuf {
   hipEvent_t ready[2];    // copy into the slot complete
   hipEvent_t freed[2];    // last reader of the slot complete
   bool freed_valid[2];    // a release was recorded for the slot
+  bool held[2];           // handed out by advance and not yet released
+  uint32_t layer[2];      // layer index last copied into the slot
   int64_t capacity;
   int staging;            // index of slot_b (the next copy target)
   hipStream_t copy;
@@ -41,6 +43,7 @@ using namespace nf4s;
 extern "C" {
 
 int32_t nf4s_host_alloc(int64_t bytes, void **out) {
+  clear_error();
   if (out == nullptr || bytes <= 0) return fail(NF4S_ERR_INVALID_ARGUMENT, "bad host_alloc args");
   *out = nullptr;
   // Pinned (page-locked) host memory allocated as such; no hipHostRegister.
@@ -50,6 +53,7 @@ int32_t nf4s_host_alloc(int64_t bytes, void **out) {
 }
 
 int32_t nf4s_host_free(void *p) {
+  clear_error();
   if (p == nullptr) return NF4S_OK;
   const hipError_t e = hipHostFree(p);
   if (e != hipSuccess) return hip_fail(e, "hipHostFree");
@@ -57,6 +61,7 @@ int32_t nf4s_host_free(void *p) {
 }
 
 int32_t nf4s_dbuf_create(int64_t slot_bytes, nf4s_dbuf **out) {
+  clear_error();
   if (out == nullptr || slot_bytes <= 0)
     return fail(NF4S_ERR_INVALID_ARGUMENT, "bad dbuf_create args");
   *out = nullptr;
@@ -86,6 +91,7 @@ int32_t nf4s_dbuf_create(int64_t slot_bytes, nf4s_dbuf **out) {
 }
 
 int32_t nf4s_dbuf_destroy(nf4s_dbuf *d) {
+  clear_error();
   if (d == nullptr) return NF4S_OK;
   hipError_t e = hipStreamSynchronize(d->copy);
   for (int i = 0; i < 2; ++i) {
@@ -105,6 +111,7 @@ int64_t nf4s_dbuf_capacity(const nf4s_dbuf *d) { return d ? d->capacity : 0; }
 // vram_double_buffer.rs:263-301.
 int32_t nf4s_dbuf_advance(nf4s_dbuf *d, uint32_t layer_idx, const void *src, int64_t len,
                           void **dev_ptr, void **ready_event) {
+  clear_error();
   if (d == nullptr || dev_ptr == nullptr || ready_event == nullptr)
     return fail(NF4S_ERR_INVALID_ARGUMENT, "bad dbuf_advance args");
   if (len < 0 || (len > 0 && src == nullptr))
@@ -113,6 +120,12 @@ int32_t nf4s_dbuf_advance(nf4s_dbuf *d, uint32_t layer_idx, const void *src, int
     return fail(NF4S_ERR_INVALID_ARGUMENT, "layer %u: src len %lld B exceeds slot capacity %lld B",
                 layer_idx, (long long)len, (long long)d->capacity);
   const int b = d->staging;
+  // The copy into a slot must wait for its last reader; without a release
+  // there is nothing to wait for (vram_double_buffer.rs:258-262).
+  if (d->held[b])
+    return fail(NF4S_ERR_INVALID_ARGUMENT,
+                "layer %u: slot still holds layer %u, which was not released", layer_idx,
+                d->layer[b]);
   hipError_t e = hipSuccess;
   if (d->freed_valid[b]) e = hipStreamWaitEvent(d->copy, d->freed[b], 0);
   if (e == hipSuccess && len > 0)
@@ -120,6 +133,8 @@ int32_t nf4s_dbuf_advance(nf4s_dbuf *d, uint32_t layer_idx, const void *src, int
   if (e == hipSuccess) e = hipEventRecord(d->ready[b], d->copy);
   if (e != hipSuccess) return hip_fail(e, "dbuf_advance");
   d->freed_valid[b] = false;
+  d->held[b] = true;
+  d->layer[b] = layer_idx;
   d->staging = b ^ 1;  // swap: the filled slot becomes the compute slot
   *dev_ptr = d->slot[b];
   *ready_event = reinterpret_cast<void *>(d->ready[b]);
@@ -130,18 +145,54 @@ int32_t nf4s_dbuf_advance(nf4s_dbuf *d, uint32_t layer_idx, const void *src, int
 // use of the slot at `dev_ptr` (a pointer nf4s_dbuf_advance returned); the
 // copy that refills that slot waits for it.
 int32_t nf4s_dbuf_release(nf4s_dbuf *d, const void *dev_ptr, void *compute_stream) {
+  clear_error();
   if (d == nullptr) return fail(NF4S_ERR_INVALID_ARGUMENT, "dbuf is NULL");
   int i = -1;
   for (int k = 0; k < 2; ++k)
     if (d->slot[k] == dev_ptr) i = k;
   if (i < 0) return fail(NF4S_ERR_INVALID_ARGUMENT, "pointer is not a slot of this buffer");
+  if (!d->held[i]) return fail(NF4S_ERR_INVALID_ARGUMENT, "slot was not handed out or is released");
   const hipError_t e = hipEventRecord(d->freed[i], as_stream(compute_stream));
   if (e != hipSuccess) return hip_fail(e, "dbuf_release");
   d->freed_valid[i] = true;
+  d->held[i] = false;
   return NF4S_OK;
 }
 
+// FlowCast::take_ready with the cuda-double-buffer feature
+// (flowcast/src/lib.rs:458-498): the pinned bytes of layer `layer_idx` are
+// copied into the staging slot on the copy stream, and the ReadyLayer names
+// the slot as slab 0 with the copy's event (ready.rs:20-52).
+int32_t nf4s_take_ready(nf4s_dbuf *d, uint32_t layer_idx, const void *pinned, int64_t len,
+                        nf4s_ready_layer *out) {
+  clear_error();
+  if (out == nullptr) return fail(NF4S_ERR_INVALID_ARGUMENT, "ReadyLayer is NULL");
+  void *ptr = nullptr, *ev = nullptr;
+  const int32_t rc = nf4s_dbuf_advance(d, layer_idx, pinned, len, &ptr, &ev);
+  if (rc != NF4S_OK) return rc;
+  out->layer_idx = layer_idx;
+  out->slab_device_ptr = ptr;
+  out->bytes = len;
+  out->copy_event = ev;
+  return NF4S_OK;
+}
+
+// FlowCast::retire_layer (flowcast/src/lib.rs:543-545): everything enqueued
+// so far on `compute_stream` is the layer's last use; the copy that refills
+// its slot waits for that.  A ReadyLayer retires once, and only while its
+// slot still holds its layer.
+int32_t nf4s_retire_layer(nf4s_dbuf *d, const nf4s_ready_layer *layer, void *compute_stream) {
+  clear_error();
+  if (d == nullptr || layer == nullptr) return fail(NF4S_ERR_INVALID_ARGUMENT, "bad args");
+  for (int k = 0; k < 2; ++k)
+    if (d->slot[k] == layer->slab_device_ptr && d->held[k] && d->layer[k] != layer->layer_idx)
+      return fail(NF4S_ERR_INVALID_ARGUMENT, "layer %u: its slot now holds layer %u",
+                  layer->layer_idx, d->layer[k]);
+  return nf4s_dbuf_release(d, layer->slab_device_ptr, compute_stream);
+}
+
 int32_t nf4s_stream_wait_event(void *stream, void *event) {
+  clear_error();
   if (event == nullptr) return fail(NF4S_ERR_INVALID_ARGUMENT, "event is NULL");
   const hipError_t e =
       hipStreamWaitEvent(as_stream(stream), reinterpret_cast<hipEvent_t>(event), 0);

@@ -23,7 +23,7 @@ import json
 import struct
 from dataclasses import dataclass, field
 from pathlib import Path
-from typing import Callable, Dict, Iterable, List, Optional, Tuple
+from typing import Callable, Dict, Iterable, List, Optional, Sequence, Tuple
 
 import torch
 
@@ -241,8 +241,14 @@ class ShardLoader:
         device; dequant_nf4_alloc length, nf4.rs:103)."""
         info = self.param_info(name)
         out = torch.empty(info.out_elems, dtype=torch.float16, device="cuda")
+        nst = ctypes.c_int64()
+        _check(_lib.load().nf4s_loader_staging_size(self._h, name.encode(), ctypes.byref(nst)))
+        staging = torch.empty(max(nst.value, 1), dtype=torch.uint8, device="cuda")
         _check(_lib.load().nf4s_loader_load_param_f16(self._h, name.encode(), out.data_ptr(),
-                                                      out.numel(), _stream_ptr(out)))
+                                                      out.numel(), staging.data_ptr(),
+                                                      nst.value, _stream_ptr(out)))
+        # Dropping `staging` here is safe: the caching allocator reuses its
+        # block for work on this same stream, which runs after the dequant.
         return out
 
     def load_param(self, name: str) -> TensorBuffer:
@@ -268,12 +274,27 @@ class ShardLoader:
             am = torch.empty(info.absmax_len, dtype=torch.float32, device="cuda")
             sc = None
         _check(_lib.load().nf4s_loader_load_param_nf4(
-            self._h, name.encode(), packed.data_ptr(), am.data_ptr(),
-            None if sc is None else sc.data_ptr(), _stream_ptr(packed)))
+            self._h, name.encode(), packed.data_ptr(), packed.numel(), am.data_ptr(),
+            am.numel() * am.element_size(), None if sc is None else sc.data_ptr(),
+            0 if sc is None else 4 * sc.numel(), _stream_ptr(packed)))
         if dq:
             return Nf4Weight(packed=packed, absmax=None, shape=shape, block_size=info.block_size,
                              absmax_q=am, absmax_scale=sc, dq_group=info.dq_group)
         return Nf4Weight(packed=packed, absmax=am, shape=shape, block_size=info.block_size)
+
+
+    def pack_layer(self, names: Sequence[str], dst_ptr: Optional[int] = None,
+                   dst_bytes: int = 0) -> Tuple[List[_lib.Nf4sBlobEntry], int]:
+        """The raw NF4 payloads of `names` packed into one host blob at
+        `dst_ptr` (pinned memory for an asynchronous H2D copy); with no
+        destination only the layout.  Returns (entries, blob bytes)."""
+        n = len(names)
+        arr = (ctypes.c_char_p * max(n, 1))(*[x.encode() for x in names])
+        ents = (_lib.Nf4sBlobEntry * max(n, 1))()
+        nb = ctypes.c_int64()
+        _check(_lib.load().nf4s_loader_pack_layer(self._h, arr, n, dst_ptr, int(dst_bytes), ents,
+                                                  ctypes.byref(nb)))
+        return list(ents)[:n], nb.value
 
 
 class PyShardLoader:

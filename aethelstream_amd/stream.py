@@ -10,12 +10,20 @@ consumed on the compute stream after waiting on the slot's ready event.
 A layer is one contiguous blob: for each matrix, its packed nibbles, uint8
 double-quant absmax codes and fp32 scales, each segment 256-byte aligned
 (``LayerLayout``), so one hipMemcpyAsync moves a whole layer.
+
+``FlowCastSeam`` is the hand-off of FlowCast's cuda-double-buffer path
+(flowcast/src/lib.rs:458-545, ready.rs:20-52): blobs packed by the shard
+loader from the on-disk NF4 payloads (``ShardLoader.pack_layer``) wait in
+pinned memory, ``take_ready`` copies one into the double buffer and returns a
+``ReadyLayer`` (slab 0 = the slot, plus the copy event), ``retire_layer``
+releases it.  Only the seam: no prefetch state machine and no file I/O
+backend (a blob is packed when first asked for).
 """
 from __future__ import annotations
 
 import ctypes
 from dataclasses import dataclass
-from typing import List, Sequence, Tuple
+from typing import Dict, List, Optional, Sequence, Tuple
 
 import torch
 
@@ -169,4 +177,116 @@ def run_stack(layers: Sequence[PinnedBuffer], layout: LayerLayout, dbuf: VramDou
         with torch.cuda.stream(stream):
             compute(l, layout.views(ptr))
         dbuf.release(ptr, stream)
+        cur = nxt
+
+
+class BlobLayout:
+    """Layout of a layer blob packed by the shard loader: one
+    ``nf4s_blob_entry`` per parameter (packed, absmax part, scales, each at
+    a 256-byte boundary) and the parameters' shapes."""
+
+    def __init__(self, names: Sequence[str], entries: Sequence[_lib.Nf4sBlobEntry],
+                 shapes: Sequence[Sequence[int]], nbytes: int):
+        self.names = list(names)
+        self.entries = list(entries)
+        self.shapes = [list(x) for x in shapes]
+        self.nbytes = int(nbytes)
+
+    def views(self, base_ptr: int) -> List[Nf4View]:
+        """Descriptors of the parameters inside a copy of the blob at base_ptr."""
+        out = []
+        for e, shape in zip(self.entries, self.shapes):
+            d = _lib.Nf4sTensor()
+            _lib.check(_lib.load().nf4s_blob_tensor(ctypes.byref(e), base_ptr, ctypes.byref(d)))
+            out.append(Nf4View(shape=shape, desc=d))
+        return out
+
+
+@dataclass
+class ReadyLayer:
+    """flowcast/src/ready.rs:20-52 with the cuda-double-buffer feature:
+    ``slab_device_ptrs`` holds (0, slot pointer); the consumer waits on
+    ``copy_event`` (``stream_wait_event``) before reading the slot, and hands
+    the layer back with ``FlowCastSeam.retire_layer``."""
+
+    layer_idx: int
+    slab_device_ptrs: List[Tuple[int, int]]
+    copy_event: int
+    views: List[Nf4View]
+    raw: _lib.Nf4sReadyLayer
+
+
+class FlowCastSeam:
+    """FlowCast::take_ready / retire_layer (flowcast/src/lib.rs:458-498,
+    543-545) over the VRAM double buffer, fed from shard-loader blobs.
+
+    ``layer_params`` maps a layer index to the names of its NF4 parameters
+    (the blob order).  Blobs are packed into pinned memory when first taken
+    (``pin``) and kept, as FlowCast's pinned pool keeps resident layers."""
+
+    def __init__(self, loader, layer_params: Dict[int, Sequence[str]]):
+        self.loader = loader
+        self.layer_params = {int(k): list(v) for k, v in layer_params.items()}
+        self.layouts: Dict[int, BlobLayout] = {}
+        for l, names in self.layer_params.items():
+            ents, nb = loader.pack_layer(names)
+            shapes = []
+            for n in names:
+                info = loader.param_info(n)
+                shapes.append(list(info.shape[:info.ndim]))
+            self.layouts[l] = BlobLayout(names, ents, shapes, nb)
+        self.pinned: Dict[int, PinnedBuffer] = {}
+        cap = max((x.nbytes for x in self.layouts.values()), default=0)
+        self.dbuf = VramDoubleBuffer(max(cap, 1))
+
+    def pin(self, layer_idx: int) -> PinnedBuffer:
+        """The layer's blob in pinned memory, packed from the shards on first use."""
+        pb = self.pinned.get(layer_idx)
+        if pb is None:
+            lay = self.layouts[layer_idx]
+            pb = PinnedBuffer(max(lay.nbytes, 1))
+            _, nb = self.loader.pack_layer(lay.names, pb.ptr, pb.nbytes)
+            assert nb == lay.nbytes
+            self.pinned[layer_idx] = pb
+        return pb
+
+    def take_ready(self, layer_idx: int) -> ReadyLayer:
+        """Issues the layer's H2D copy on the copy stream; returns the ReadyLayer."""
+        lay = self.layouts[layer_idx]
+        pb = self.pin(layer_idx)
+        raw = _lib.Nf4sReadyLayer()
+        _lib.check(_lib.load().nf4s_take_ready(self.dbuf.handle, layer_idx, pb.ptr, lay.nbytes,
+                                               ctypes.byref(raw)))
+        return ReadyLayer(layer_idx=layer_idx, slab_device_ptrs=[(0, raw.slab_device_ptr)],
+                          copy_event=raw.copy_event, views=lay.views(raw.slab_device_ptr),
+                          raw=raw)
+
+    def retire_layer(self, layer: ReadyLayer, stream: torch.cuda.Stream) -> None:
+        """The work enqueued so far on `stream` is the layer's last use."""
+        _lib.check(_lib.load().nf4s_retire_layer(self.dbuf.handle, ctypes.byref(layer.raw),
+                                                 stream.cuda_stream))
+
+    def close(self) -> None:
+        self.dbuf.close()
+        for pb in self.pinned.values():
+            pb.close()
+        self.pinned.clear()
+
+
+def stream_layers(seam: FlowCastSeam, order: Sequence[int], compute,
+                  stream: torch.cuda.Stream) -> None:
+    """The consumer loop of the double pass over the seam: the next layer's
+    copy is issued before the current layer's kernels, the compute stream
+    waits on each copy event, and each layer retires after its kernels.
+    ``compute(layer_idx, views)`` enqueues the kernels on the current stream."""
+    order = list(order)
+    if not order:
+        return
+    cur = seam.take_ready(order[0])
+    for i, l in enumerate(order):
+        nxt = seam.take_ready(order[i + 1]) if i + 1 < len(order) else None
+        stream_wait_event(stream, cur.copy_event)
+        with torch.cuda.stream(stream):
+            compute(l, cur.views)
+        seam.retire_layer(cur, stream)
         cur = nxt

@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define NF4S_ABI_VERSION 1
+#define NF4S_ABI_VERSION 2
 
 enum nf4s_status {
     NF4S_OK = 0,
@@ -67,8 +67,10 @@ int32_t nf4s_abi_version(void);
 /* Static description of a status code. */
 const char *nf4s_strerror(int32_t status);
 
-/* Message of the last failing call on this host thread (the reference's
- * MalformedIndex detail text, e.g. "absmax too small: 3 < 4"). */
+/* Message of the last call made on this host thread: the reason it failed
+ * (the reference's MalformedIndex detail text, e.g. "absmax too small:
+ * 3 < 4"), or "" when it succeeded.  Every status-returning call clears it
+ * first. */
 const char *nf4s_last_error_message(void);
 
 /*
@@ -228,8 +230,9 @@ int32_t nf4s_gemm_fwd_workspace_size(const int64_t *ns, int32_t count, int64_t m
  * (doublepass/src/backward.rs:87-93, 117-129, 160-168, 284-300); accumulate
  * is the micro-batch sum of backward.rs:478-502.  dy [m, n] and x [m, k] are
  * row-major bf16 with n % 8 == 0 and k % 8 == 0, 16-byte aligned; dw [n, k]
- * row-major fp32.  dy and x must each be below 2 GiB.  No NF4 operand: this
- * is the plain bf16 GEMM the backward pass needs beside the fused ones.
+ * row-major fp32.  dy and x must each be below 2 GiB with m rounded up to a
+ * multiple of 64.  No NF4 operand: this is the plain bf16 GEMM the backward
+ * pass needs beside the fused ones.
  */
 int32_t nf4s_gemm_wgrad(const void *dy, const void *x, int64_t m, int64_t n,
                         int64_t k, float *dw, int32_t accumulate, void *stream);
@@ -259,8 +262,9 @@ int64_t nf4s_dbuf_capacity(const nf4s_dbuf *d);
  * slots and returns the new compute slot and its event.  The consumer must
  * make its compute stream wait on `*ready_event` (nf4s_stream_wait_event)
  * before reading `*dev_ptr` (flowcast/src/ready.rs:16-19,43-51).  Fails
- * when len exceeds the slot capacity (vram_double_buffer.rs:269-275).  The
- * slot returned at call N is refilled at call N+2, after the copy stream has
+ * when len exceeds the slot capacity (vram_double_buffer.rs:269-275), and
+ * when the staging slot was handed out and not released yet.  The slot
+ * returned at call N is refilled at call N+2, after the copy stream has
  * waited for the release recorded for it.
  */
 int32_t nf4s_dbuf_advance(nf4s_dbuf *d, uint32_t layer_idx, const void *src,
@@ -268,8 +272,32 @@ int32_t nf4s_dbuf_advance(nf4s_dbuf *d, uint32_t layer_idx, const void *src,
 
 /* Records that everything enqueued so far on `compute_stream` is the last use
  * of the slot at `dev_ptr` (returned by nf4s_dbuf_advance); the copy that
- * refills that slot waits for this. */
+ * refills that slot waits for this.  Once per advance. */
 int32_t nf4s_dbuf_release(nf4s_dbuf *d, const void *dev_ptr, void *compute_stream);
+
+/* FlowCast's ReadyLayer (flowcast/src/ready.rs:20-52) with the
+ * cuda-double-buffer feature: slab 0 is the double-buffer slot holding the
+ * layer's blob, and the consumer must make its compute stream wait on
+ * `copy_event` before reading it (ready.rs:16-19). */
+typedef struct nf4s_ready_layer {
+    uint32_t layer_idx;
+    void *slab_device_ptr;   /* slab 0 (ready.rs:32-36) */
+    int64_t bytes;           /* blob bytes copied into the slot */
+    void *copy_event;        /* hipEvent_t (ready.rs:43-51) */
+} nf4s_ready_layer;
+
+/* FlowCast::take_ready (flowcast/src/lib.rs:458-498) over the double buffer:
+ * nf4s_dbuf_advance of the layer's pinned blob, returned as a ReadyLayer.
+ * Fails like nf4s_dbuf_advance (capacity; a staging slot whose previous
+ * layer was not retired). */
+int32_t nf4s_take_ready(nf4s_dbuf *d, uint32_t layer_idx, const void *pinned,
+                        int64_t len, nf4s_ready_layer *out);
+
+/* FlowCast::retire_layer (flowcast/src/lib.rs:543-545): the work enqueued so
+ * far on `compute_stream` is the layer's last use (nf4s_dbuf_release of its
+ * slot).  Fails for a layer already retired or whose slot was refilled. */
+int32_t nf4s_retire_layer(nf4s_dbuf *d, const nf4s_ready_layer *layer,
+                          void *compute_stream);
 
 /* hipStreamWaitEvent on a ready event returned by nf4s_dbuf_advance. */
 int32_t nf4s_stream_wait_event(void *stream, void *event);
@@ -311,20 +339,60 @@ int32_t nf4s_loader_param_info(nf4s_loader *l, const char *name, nf4s_param_info
 int32_t nf4s_loader_load_layer(nf4s_loader *l, uint32_t layer, const uint8_t **data,
                                int64_t *len);
 
+/* Device staging bytes nf4s_loader_load_param_f16 needs for `name`: the
+ * packed bytes, absmax part and scales at 256-byte boundaries (0 for an fp16
+ * entry).  Allocates nothing. */
+int32_t nf4s_loader_staging_size(nf4s_loader *l, const char *name, int64_t *bytes);
+
 /* ShardLoader::load_param (loader.rs:78-206) into a device f16 buffer of
  * out_len elements: NF4 entries pass the reference's checks in its order
- * (loader.rs:99-151) and are dequantized on the device with
- * dequant_nf4_alloc semantics (2 * packed bytes elements, nf4.rs:98-107);
- * fp16 entries are copied (loader.rs:179-198). */
+ * (loader.rs:99-151), are copied into the caller's 16-byte aligned device
+ * `staging` buffer (at least nf4s_loader_staging_size bytes) and dequantized
+ * on the device with dequant_nf4_alloc semantics (2 * packed bytes elements,
+ * nf4.rs:98-107); fp16 entries are copied (loader.rs:179-198).  Calls that
+ * share a staging buffer must not overlap (one stream, or ordered streams). */
 int32_t nf4s_loader_load_param_f16(nf4s_loader *l, const char *name, uint16_t *out,
-                                   int64_t out_len, void *stream);
+                                   int64_t out_len, void *staging, int64_t staging_bytes,
+                                   void *stream);
 
 /* The raw NF4 payload of a parameter (packed bytes, fp32 absmax or uint8
- * codes, fp32 scales) copied into caller device buffers, for a weight
- * provider that keeps NF4 resident instead of widening it to f32
- * (doublepass/src/shard_provider.rs:103-130). */
+ * codes, fp32 scales) copied into caller device buffers of the given byte
+ * capacities, for a weight provider that keeps NF4 resident instead of
+ * widening it to f32 (doublepass/src/shard_provider.rs:103-130).  The fp32
+ * parts copy floor(length / 4) floats, what the reference reads
+ * (loader.rs:158-161); `scale` is NULL (capacity 0) without double-quant. */
 int32_t nf4s_loader_load_param_nf4(nf4s_loader *l, const char *name, uint8_t *packed,
-                                   void *absmax_or_q, float *scale, void *stream);
+                                   int64_t packed_bytes, void *absmax_or_q,
+                                   int64_t absmax_bytes, float *scale, int64_t scale_bytes,
+                                   void *stream);
+
+/* Placement of one NF4 parameter in a layer blob, byte offsets from the
+ * blob start; each part begins at a 256-byte boundary. */
+typedef struct nf4s_blob_entry {
+    int64_t packed_off;
+    int64_t packed_len;    /* bytes */
+    int64_t absmax_off;    /* fp32 absmax, or uint8 double-quant codes */
+    int64_t absmax_len;    /* entries */
+    int64_t scale_off;     /* fp32 double-quant scales (0 without) */
+    int64_t scale_len;     /* entries (0 without double-quant) */
+    int32_t block_size;
+    int32_t dq_group;      /* 0 without double-quant */
+} nf4s_blob_entry;
+
+/* The bytes a FlowCast pinned slot holds for one layer
+ * (flowcast/src/ready.rs:27-30): the raw NF4 payloads of `count` parameters
+ * (e.g. a layer's 7 matrices) copied from the mmap'd shards into one host
+ * blob `dst` (pinned, so that nf4s_take_ready copies it asynchronously),
+ * parts placed as nf4s_blob_entry says.  With dst == NULL only `entries` and
+ * *bytes are filled (a size query).  Entries pass the checks of
+ * nf4s_loader_load_param_nf4. */
+int32_t nf4s_loader_pack_layer(nf4s_loader *l, const char *const *names, int32_t count,
+                               void *dst, int64_t dst_bytes, nf4s_blob_entry *entries,
+                               int64_t *bytes);
+
+/* Descriptor of blob entry `e` inside a copy of the blob at `base` (e.g. the
+ * slab of a ReadyLayer). */
+int32_t nf4s_blob_tensor(const nf4s_blob_entry *e, const void *base, nf4s_tensor *out);
 
 #ifdef __cplusplus
 }

@@ -30,7 +30,8 @@ def test_header_symbols_exported():
 
 def test_abi_version_and_strerror():
     lib = _lib.load()
-    assert lib.nf4s_abi_version() == 1
+    hdr = open(HEADER).read()
+    assert lib.nf4s_abi_version() == int(re.search(r"#define NF4S_ABI_VERSION (\d+)", hdr).group(1))
     assert lib.nf4s_strerror(0) == b"ok"
     assert b"nf4_absmax" in lib.nf4s_strerror(_lib.NF4S_ERR_ABSMAX_TOO_SMALL)
     assert b"nf4_packed" in lib.nf4s_strerror(_lib.NF4S_ERR_PACKED_TOO_SMALL)
@@ -135,3 +136,12 @@ def test_requantize_argument_rejection():
     assert lib.nf4s_quantize_dq_bf16(p, 128, 64, 16384, p, p, p, None) == _lib.NF4S_ERR_INVALID_ARGUMENT
     assert lib.nf4s_quantize_bf16(p, 128, 32, p, p, None) == _lib.NF4S_ERR_UNSUPPORTED_SHAPE
     assert lib.nf4s_quantize_dq(p, -1, 64, 256, p, p, p, None) == _lib.NF4S_ERR_INVALID_ARGUMENT
+
+
+def test_wgrad_rejects_offsets_past_2gib_in_the_last_step():
+    # m = 1 with n = 2^24: dy itself is 32 MiB, but the last 64-token step
+    # addresses rows up to 63, 2 GiB into dy, where 32-bit lane offsets wrap.
+    lib = _lib.load()
+    rc = lib.nf4s_gemm_wgrad(0x1000, 0x2000, 1, 1 << 24, 8, 0x3000, 0, None)
+    assert rc == _lib.NF4S_ERR_UNSUPPORTED_SHAPE
+    assert b"m rounded up to 64" in lib.nf4s_last_error_message()

@@ -255,3 +255,26 @@ def test_double_rounding_ties(kind, bs):
     f16 = kind == "f16"
     ref = (oracle.dequant_f16 if f16 else oracle.dequant_bf16)(pk, am, n, bs)
     np.testing.assert_array_equal(_gpu_dequant(pk, am, n, bs, f16), ref)
+
+
+def test_dq_planted_ties_round_half_even_on_device():
+    """The planted x.5 quotients of tests/test_oracle.py on the device: the
+    standalone encoder and the fused quantize + double-quant launch (whose
+    block absmax are the planted values) both round half to even by a true
+    division, bit-equal to the oracle."""
+    from test_oracle import _dq_tie_vector, dq_tie_expected
+    a, ks = _dq_tie_vector()
+    q_ref, s_ref = oracle.dq_encode(a, 256)
+    np.testing.assert_array_equal(q_ref[257:384], dq_tie_expected(ks))
+    q, sc = nf4.dq_encode(_dev(a), 256)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(q.cpu().numpy(), q_ref)
+    np.testing.assert_array_equal(sc.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
+    # Block b holds a[b] at element 0 and zeros elsewhere: its absmax is a[b].
+    x = np.zeros((a.size, 64), np.float32)
+    x[:, 0] = a
+    w = nf4.quantize_weight(_dev(x), double_quant=True)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(w.absmax_q.cpu().numpy(), q_ref)
+    np.testing.assert_array_equal(w.absmax_scale.cpu().numpy().view(np.uint32),
+                                  s_ref.view(np.uint32))

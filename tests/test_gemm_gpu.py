@@ -442,3 +442,26 @@ def test_xcd_pair_tile_order(m, wide):
     torch.cuda.synchronize()
     assert rel_l2(dx.float().cpu().numpy(), ref.cpu().numpy()) <= TOL_SAME
 
+
+
+@pytest.mark.parametrize("name,ns,k", [("[q,k,v]", [8192, 1024, 1024], 8192),
+                                       ("[gate,up]", [28672, 28672], 8192)])
+def test_fwd_grouped_70b_launches(name, ns, k):
+    """The grouped launches config 4 times, at their size (M = 8192): the
+    [q,k,v] launch (1280 tiles, 5 whole rounds) and the [gate,up] launch
+    (XCD-pair tile order across two groups).  Bit-equal to separate unsplit
+    launches of each weight, and within the bf16 output rounding of fp32."""
+    m = 8192
+    g = torch.Generator(device=DEV).manual_seed(81)
+    ws = [nf4.quantize_weight(torch.randn(n, k, device=DEV, generator=g) * 0.02, double_quant=True)
+          for n in ns]
+    x = torch.randn(m, k, device=DEV, generator=g).to(torch.bfloat16)
+    ys = gemm.linear_fwd_grouped(x, ws)
+    for y, w in zip(ys, ws):
+        sep = gemm.linear_fwd(x, w, split_k=False)
+        assert torch.equal(y.view(torch.int16), sep.view(torch.int16)), name
+        ref = x.float() @ nf4.dequant(w).float().t()
+        err = ((y.float() - ref).norm() / ref.norm()).item()
+        assert err <= TOL_SAME, (name, err)
+        del sep, ref
+    torch.cuda.synchronize()

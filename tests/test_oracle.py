@@ -168,6 +168,45 @@ def test_dq_invariants():
     assert np.all(np.abs(dec - a) <= s[np.arange(a.size) // 256] * 0.5 * (1 + 1e-6))
 
 
+def _dq_tie_vector():
+    """Absmax values whose quotient by the group scale is exactly k + 0.5.
+    Group 0: max 127 -> scale 1.0, a = k + 0.5.  Group 1: max 889 -> scale
+    7.0 (exact), a = 7(k + 0.5), also exact; there a * fl(1/7) rounds to
+    another integer for 39 of the 127 k, so a reciprocal multiply in place of
+    the division shows."""
+    ks = np.arange(0, 127, dtype=np.float32)
+    g0 = np.concatenate([[np.float32(127.0)], ks + np.float32(0.5)])
+    g1 = np.concatenate([[np.float32(889.0)], np.float32(7.0) * (ks + np.float32(0.5))])
+    a = np.zeros(512, np.float32)
+    a[:g0.size] = g0
+    a[256:256 + g1.size] = g1
+    return a, ks
+
+
+def dq_tie_expected(ks):
+    """Round half to even of k + 0.5 is the even one of k and k + 1."""
+    k = ks.astype(np.int64)
+    return np.where(k % 2 == 0, k, k + 1).astype(np.uint8)
+
+
+def test_dq_planted_ties_round_half_even():
+    # The double-quant spec rounds a / scale half to even (the RNE of
+    # ramflow/src/kernels/mod.rs:96-110), not half away from zero like the
+    # .round() of galore/src/quantize.rs:22: on x.5 quotients the two differ
+    # for every even k.
+    a, ks = _dq_tie_vector()
+    q, s = oracle.dq_encode(a, 256)
+    assert s[0] == np.float32(1.0) and s[1] == np.float32(7.0)
+    want = dq_tie_expected(ks)
+    np.testing.assert_array_equal(q[1:128], want)
+    np.testing.assert_array_equal(q[257:384], want)
+    assert q[0] == 127 and q[256] == 127
+    half_away = np.floor(ks + np.float32(0.5) + 0.5).astype(np.uint8)
+    assert np.count_nonzero(half_away != want) == 64   # k = 0, 2, ..., 126
+    recip = np.rint(a[257:384] * (np.float32(1.0) / np.float32(7.0))).astype(np.uint8)
+    assert np.count_nonzero(recip != want) == 39
+
+
 def test_matmul_tb_and_dgrad_against_fp64():
     rng = np.random.default_rng(3)
     a = rng.standard_normal((5, 37)).astype(np.float32)

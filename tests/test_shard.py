@@ -21,10 +21,11 @@ def shard_dir(tmp_path):
     return tmp_path / "m", index, registry, tensors
 
 
-def _load_f16_status(loader, name):
-    """Calls load_param_f16 with a dummy device pointer: the checks must fail
-    before the pointer is used."""
-    return _lib.load().nf4s_loader_load_param_f16(loader._h, name.encode(), 0x1000, 1 << 20, None)
+def _load_f16_status(loader, name, staging_bytes=1 << 20):
+    """Calls load_param_f16 with dummy device pointers: the checks must fail
+    before either pointer is used."""
+    return _lib.load().nf4s_loader_load_param_f16(loader._h, name.encode(), 0x1000, 1 << 20,
+                                                  0x2000, staging_bytes, None)
 
 
 def test_param_info_and_pyo3_mirror(shard_dir):
@@ -123,3 +124,136 @@ def test_malformed_nf4_entries(shard_dir, mutation, match):
     assert msg.startswith("malformed index entry 'model.layers.0.q': ")
     import re
     assert re.search(match, msg), msg
+
+
+@pytest.mark.parametrize("field,value", [
+    ("byte_offset", -8), ("byte_length", -1), ("nf4_absmax_offset", -8),
+    ("nf4_absmax_length", -8), ("nf4_block_size", -64),
+])
+def test_negative_sizes_are_json_errors(shard_dir, field, value):
+    # usize / Option<usize> fields (index.rs:7-34): serde rejects a negative
+    # integer when IndexStore::load parses the index, before any access.
+    d, index, registry, _ = shard_dir
+    e = dict(index["model.layers.0.q"])
+    e[field] = value
+    index = dict(index)
+    index["model.layers.0.q"] = e
+    write_index(d, index, registry)
+    with pytest.raises(shard.ShardJsonError, match=f"invalid value: integer `{value}`"):
+        shard.ShardLoader(d)
+
+
+def test_negative_offset_with_matching_length_does_not_wrap(shard_dir):
+    # offset -8 + length 8 sums to 0 in unsigned arithmetic; the entry must
+    # still be rejected (here already at parse time).
+    d, index, registry, _ = shard_dir
+    e = dict(index["model.layers.0.q"])
+    e.update(nf4_absmax_offset=-8, nf4_absmax_length=8)
+    index = dict(index)
+    index["model.layers.0.q"] = e
+    write_index(d, index, registry)
+    with pytest.raises(shard.ShardJsonError):
+        shard.ShardLoader(d)
+
+
+def test_huge_offset_is_out_of_bounds(shard_dir):
+    # An offset near 2^64 - 1 as unsigned must not wrap the bounds check.
+    d, index, registry, _ = shard_dir
+    e = dict(index["model.layers.0.q"])
+    e.update(nf4_absmax_offset=(1 << 63) - 4, nf4_absmax_length=8)
+    index = dict(index)
+    index["model.layers.0.q"] = e
+    write_index(d, index, registry)
+    L = shard.ShardLoader(d)
+    assert _load_f16_status(L, "model.layers.0.q") == _lib.NF4S_ERR_MALFORMED_INDEX
+    assert "absmax data out of bounds" in _lib.load().nf4s_last_error_message().decode()
+
+
+def test_staging_size_and_too_small_staging(shard_dir):
+    d, index, _, _ = shard_dir
+    L = shard.ShardLoader(d)
+    n = ctypes.c_int64()
+    _lib.check(_lib.load().nf4s_loader_staging_size(L._h, b"model.layers.0.q", ctypes.byref(n)))
+    e = index["model.layers.0.q"]
+    rnd = lambda x: (x + 255) // 256 * 256
+    assert n.value == rnd(e["byte_length"]) + rnd(e["nf4_absmax_length"])
+    _lib.check(_lib.load().nf4s_loader_staging_size(L._h, b"model.layers.0.norm",
+                                                   ctypes.byref(n)))
+    assert n.value == 0
+    rc = _load_f16_status(L, "model.layers.0.q", staging_bytes=255)
+    assert rc == _lib.NF4S_ERR_INVALID_ARGUMENT
+    assert "staging holds 255 bytes" in _lib.load().nf4s_last_error_message().decode()
+
+
+def test_nf4_destination_capacity_checked(shard_dir):
+    d, index, _, _ = shard_dir
+    L = shard.ShardLoader(d)
+    e = index["model.layers.0.q"]
+    rc = _lib.load().nf4s_loader_load_param_nf4(L._h, b"model.layers.0.q", 0x1000,
+                                                e["byte_length"] - 1, 0x2000, 1 << 20, None, 0,
+                                                None)
+    assert rc == _lib.NF4S_ERR_INVALID_ARGUMENT
+    assert "destination too small" in _lib.load().nf4s_last_error_message().decode()
+
+
+def test_last_error_message_cleared_by_a_successful_call(shard_dir):
+    d, _, _, _ = shard_dir
+    lib = _lib.load()
+    L = shard.ShardLoader(d)
+    info = _lib.Nf4sParamInfo()
+    assert lib.nf4s_loader_param_info(L._h, b"nope", ctypes.byref(info)) == \
+        _lib.NF4S_ERR_PARAM_NOT_FOUND
+    assert b"not found" in lib.nf4s_last_error_message()
+    _lib.check(lib.nf4s_loader_param_info(L._h, b"model.layers.0.q", ctypes.byref(info)))
+    assert lib.nf4s_last_error_message() == b""
+    # The same for a call outside the loader (host-only validation path).
+    assert lib.nf4s_gemm_fwd_workspace_size(None, 1, 1, 64, None) == _lib.NF4S_ERR_INVALID_ARGUMENT
+    assert lib.nf4s_last_error_message() != b""
+    ns = (ctypes.c_int64 * 1)(128)
+    nb = ctypes.c_int64()
+    _lib.check(lib.nf4s_gemm_fwd_workspace_size(ns, 1, 0, 64, ctypes.byref(nb)))
+    assert lib.nf4s_last_error_message() == b""
+
+
+@pytest.mark.parametrize("double_quant", [False, True])
+def test_pack_layer_blob_bytes_and_descriptors(tmp_path, double_quant):
+    # The blob a FlowCast pinned slot holds for a layer: each parameter's raw
+    # payload parts at 256-byte boundaries, byte-equal to the shard's
+    # tensors; descriptors rebased on any copy of the blob.
+    d = tmp_path / "m"
+    index, _, tensors = build_cpu_shards(d, n_layers=2, dim=128, double_quant=double_quant)
+    L = shard.ShardLoader(d)
+    names = ["model.layers.0.q", "model.layers.1.q"]
+    ents, nb = L.pack_layer(names)
+    assert nb % 256 == 0 and ents[0].packed_off == 0
+    buf = (ctypes.c_uint8 * nb)()
+    base = ctypes.addressof(buf)
+    ents2, nb2 = L.pack_layer(names, base, nb)
+    assert nb2 == nb
+    raw = bytes(buf)
+    from safetensors.numpy import load_file
+    from aethelstream_amd import stream as st
+    lay = st.BlobLayout(names, ents2, [[128, 128]] * 2, nb)
+    for e, v, name, l in zip(ents2, lay.views(base), names, range(2)):
+        for off in (e.packed_off, e.absmax_off, e.scale_off):
+            assert off % 256 == 0
+        f = load_file(str(d / f"layer_{l}.safetensors"))
+        assert raw[e.packed_off:e.packed_off + e.packed_len] == f[f"{name}.__packed__"].tobytes()
+        if double_quant:
+            assert e.dq_group == 256 and e.absmax_len == 128 * 128 // 64
+            assert raw[e.absmax_off:e.absmax_off + e.absmax_len] == \
+                f[f"{name}.__absmax_q__"].tobytes()
+            assert raw[e.scale_off:e.scale_off + 4 * e.scale_len] == \
+                f[f"{name}.__absmax_scale__"].tobytes()
+            assert v.desc.absmax is None and v.desc.absmax_q == base + e.absmax_off
+            assert v.desc.absmax_scale == base + e.scale_off and v.desc.scale_len == 1
+        else:
+            assert e.dq_group == 0 and e.scale_len == 0
+            assert raw[e.absmax_off:e.absmax_off + 4 * e.absmax_len] == \
+                f[f"{name}.__absmax__"].tobytes()
+            assert v.desc.absmax == base + e.absmax_off and v.desc.absmax_q is None
+        assert v.desc.packed == base + e.packed_off and v.desc.packed_len == e.packed_len
+    with pytest.raises(_lib.Nf4sError, match="blob holds 256 bytes"):
+        L.pack_layer(names, base, 256)
+    with pytest.raises(shard.MalformedIndexEntry, match="not nf4"):
+        L.pack_layer(["model.layers.0.norm"])

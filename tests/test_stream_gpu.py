@@ -91,3 +91,145 @@ def test_layer_blob_roundtrip():
         torch.cuda.synchronize()
         assert torch.equal(a, b)
     pb.close()
+
+
+LAYER_SHAPES = [("q", 256, 256), ("k", 64, 256), ("v", 64, 256), ("o", 256, 256),
+                ("gate", 512, 256), ("up", 512, 256), ("down", 256, 512)]
+
+
+def _write_model(root, n_layers, seed):
+    from aethelstream_amd import shard
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    layers = {l: [(f"model.layers.{l}.{nm}", torch.randn(r, c, device="cuda", generator=g) * 0.02)
+                  for nm, r, c in LAYER_SHAPES] for l in range(n_layers)}
+    shard.write_shards(layers, root, double_quant=True)
+    return {l: [nm for nm, _ in ps] for l, ps in layers.items()}
+
+
+def _layer_fwd(x, hid, views, outs):
+    gemm.linear_fwd_grouped(x, views[0:3], outs[0:3])
+    gemm.linear_fwd(x, views[3], outs[3])
+    gemm.linear_fwd_grouped(x, views[4:6], outs[4:6])
+    gemm.linear_fwd(hid, views[6], outs[6])
+
+
+def test_flowcast_seam_streams_shard_layers(tmp_path):
+    """Layers written by write_shards, packed from the shard files into pinned
+    blobs by the loader, streamed through take_ready / retire_layer: each
+    layer's 7 outputs equal the outputs over the same weights loaded resident
+    (load_param_nf4), bit for bit."""
+    from aethelstream_amd import shard
+    n, m = 6, 320
+    names = _write_model(tmp_path, n, seed=21)
+    L = shard.ShardLoader(tmp_path)
+    g = torch.Generator(device="cuda").manual_seed(22)
+    x = torch.randn(m, 256, device="cuda", generator=g).to(torch.bfloat16)
+    hid = torch.randn(m, 512, device="cuda", generator=g).to(torch.bfloat16)
+    ref = []
+    for l in range(n):
+        ws = [L.load_param_nf4(nm) for nm in names[l]]
+        outs = [torch.empty(m, r, dtype=torch.bfloat16, device="cuda") for _, r, _ in LAYER_SHAPES]
+        _layer_fwd(x, hid, ws, outs)
+        ref.append(outs)
+    seam = st.FlowCastSeam(L, names)
+    got = [[torch.full((m, r), float("nan"), dtype=torch.bfloat16, device="cuda")
+            for _, r, _ in LAYER_SHAPES] for _ in range(n)]
+    stream = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    # Forward order, then the recompute's reverse order (double pass).
+    order = list(range(n)) + list(reversed(range(n)))
+    seen = []
+
+    def compute(l, views):
+        seen.append(l)
+        _layer_fwd(x, hid, views, got[l])
+
+    st.stream_layers(seam, order, compute, stream)
+    torch.cuda.synchronize()
+    assert seen == order
+    for l in range(n):
+        for a, b in zip(got[l], ref[l]):
+            assert torch.equal(a, b), f"layer {l} differs"
+    # Protocol errors: a second retire, and a take_ready into a slot whose
+    # layer was never retired.
+    r0 = seam.take_ready(0)
+    stream_c = torch.cuda.current_stream()
+    st.stream_wait_event(stream_c, r0.copy_event)
+    seam.retire_layer(r0, stream_c)
+    with pytest.raises(_lib.Nf4sError, match="not handed out or is released"):
+        seam.retire_layer(r0, stream_c)
+    r1 = seam.take_ready(1)
+    seam.take_ready(2)                       # the slot r0 held, released
+    with pytest.raises(_lib.Nf4sError, match="which was not released"):
+        seam.take_ready(3)                   # r1's slot: still held
+    st.stream_wait_event(stream_c, r1.copy_event)
+    seam.retire_layer(r1, stream_c)
+    torch.cuda.synchronize()
+    seam.close()
+    L.close()
+
+
+LAYER_70B = [("q", 8192, 8192), ("k", 1024, 8192), ("v", 1024, 8192), ("o", 8192, 8192),
+             ("gate", 28672, 8192), ("up", 28672, 8192), ("down", 8192, 28672)]
+
+
+def test_config5_80_streamed_70b_layers():
+    """BASELINE config 5 at its workload: 80 double-quantized 70B-shaped
+    layers (441 MB blobs) in pinned memory, 4096 tokens, streamed through the
+    double buffer while the previous layer's fused forwards run.  The blobs
+    alternate between two distinct layers, so a slot read before its copy
+    completed (or refilled before its last reader finished) shows as the
+    other layer's outputs.  Each layer's 7 outputs are compared on the compute
+    stream, in stream order, with the resident outputs of its blob before the
+    next layer overwrites them; one layer is also checked against fp32."""
+    M, nlayers = 4096, 80
+    layout = st.LayerLayout(LAYER_70B)
+    assert layout.nbytes == 441397248
+    g = torch.Generator(device="cuda").manual_seed(50)
+    distinct = []
+    for s in range(2):
+        gw = torch.Generator(device="cuda").manual_seed(100 + s)
+        distinct.append([nf4.quantize_weight(torch.randn(r, c, device="cuda", generator=gw) * 0.02,
+                                             double_quant=True) for _, r, c in LAYER_70B])
+    print(f"config5: packing {nlayers} pinned blobs of {layout.nbytes} B", flush=True)
+    host = []
+    for l in range(nlayers):
+        pb = st.PinnedBuffer(layout.nbytes)
+        layout.pack_into(pb.tensor, distinct[l % 2])
+        host.append(pb)
+    x = torch.randn(M, 8192, device="cuda", generator=g).to(torch.bfloat16)
+    hid = torch.randn(M, 28672, device="cuda", generator=g).to(torch.bfloat16)
+    ins = [x, x, x, x, x, x, hid]
+    ref = []
+    for ws in distinct:
+        outs = [torch.empty(M, r, dtype=torch.bfloat16, device="cuda") for _, r, _ in LAYER_70B]
+        _layer_fwd(x, hid, ws, outs)
+        ref.append(outs)
+    outs = [torch.full((M, r), float("nan"), dtype=torch.bfloat16, device="cuda")
+            for _, r, _ in LAYER_70B]
+    bad = torch.zeros(nlayers, dtype=torch.int32, device="cuda")
+    dbuf = st.VramDoubleBuffer(layout.nbytes)
+    stream = torch.cuda.Stream()
+
+    def compute(l, views):
+        _layer_fwd(x, hid, views, outs)
+        # On the compute stream, before layer l+1's kernels are enqueued.
+        diff = torch.stack([(a != b).any() for a, b in zip(outs, ref[l % 2])])
+        bad[l] = diff.to(torch.int32).sum()
+
+    torch.cuda.synchronize()
+    print("config5: streaming", flush=True)
+    st.run_stack(host, layout, dbuf, compute, stream)
+    torch.cuda.synchronize()
+    assert bad.sum().item() == 0, f"layers with differing outputs: {bad.nonzero().flatten().tolist()}"
+    # The resident outputs of blob 0 (equal to streamed layers 0, 2, ...)
+    # against fp32 over the dequantized weights.
+    for (nm, r, c), w, a, y in zip(LAYER_70B, distinct[0], ins, ref[0]):
+        wf = nf4.dequant(w).float()
+        yf = a.float() @ wf.t()
+        rel = ((y.float() - yf).norm() / yf.norm()).item()
+        assert rel <= 4e-3, f"{nm}: rel-L2 {rel:.3e} vs fp32"
+        del wf, yf
+    dbuf.close()
+    for pb in host:
+        pb.close()
