@@ -114,6 +114,8 @@ SIGNATURES = {
                                         _I64, _I64, _P, _I64, _P]),
     "nf4s_gemm_fwd_workspace_size": (_I32, [ctypes.POINTER(_I64), _I32, _I64, _I64,
                                             ctypes.POINTER(_I64)]),
+    "nf4s_gemm_fwd_grouped_noalloc": (_I32, [_P, _TP, ctypes.POINTER(_I64), ctypes.POINTER(_P),
+                                             _I32, _I64, _I64, _P]),
     "nf4s_gemm_wgrad": (_I32, [_P, _P, _I64, _I64, _I64, _P, _I32, _P]),
     "nf4s_host_alloc": (_I32, [_I64, ctypes.POINTER(_P)]),
     "nf4s_host_free": (_I32, [_P]),

@@ -26,6 +26,7 @@
 // accumulator layout is lane l: column l % 32, row 8(v/4) + 4g + v%4; the
 // weight fragment is the first operand, so the accumulator's columns are
 // activation rows and its rows are output columns.
+#include <mutex>
 #include <type_traits>
 
 #include "abi_common.hpp"
@@ -1559,6 +1560,39 @@ static int64_t fwd_workspace_bytes(const int64_t *ns, int32_t count, int64_t m, 
   return best;
 }
 
+// Split-K workspace of nf4s_gemm_fwd_grouped_noalloc: a file-scope device
+// array, one copy per GPU, held until the process ends.  A plan never needs
+// more partial tiles than the device has CUs (S <= CUs / r slices for r tail
+// tiles), so 256 partial tiles (64 MiB) cover every shape on a 256-CU MI355X.
+constexpr int64_t kScratchTiles = 256;
+constexpr int64_t kScratchBytes = kScratchTiles * kPartialFloats * (int64_t)sizeof(float);
+static __device__ __align__(256) float scratch[kScratchTiles * kPartialFloats];
+
+// Device address of this GPU's `scratch`, looked up with the device current
+// on the first call made on it.  The host-side name is only a stand-in
+// handle: kernels get this address, never the name.
+static int32_t scratch_on_current_device(void **out) {
+  constexpr int kMaxDevices = 64;
+  static std::mutex mu;
+  static void *addr[kMaxDevices];
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(NF4S_ERR_HIP, "hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(NF4S_ERR_UNSUPPORTED_SHAPE, "device %d beyond the %d the scratch table holds",
+                dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(mu);
+  if (addr[dev] == nullptr) {
+    void *p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return fail(NF4S_ERR_HIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+    addr[dev] = p;
+  }
+  *out = addr[dev];
+  return NF4S_OK;
+}
+
 }  // namespace nf4s
 
 using namespace nf4s;
@@ -1610,6 +1644,26 @@ int32_t nf4s_gemm_fwd_workspace_size(const int64_t *ns, int32_t count, int64_t m
     return fail(NF4S_ERR_INVALID_ARGUMENT, "count must be 1..%d with sizes", kMaxGroups);
   *bytes = fwd_workspace_bytes(ns, count, m, k);
   return NF4S_OK;
+}
+
+// nf4s_gemm_fwd_grouped_ws with the library's static per-GPU scratch as the
+// workspace: no allocation, for callers that cannot allocate.
+int32_t nf4s_gemm_fwd_grouped_noalloc(const uint16_t *x, const nf4s_tensor *ws, const int64_t *ns,
+                                      uint16_t *const *ys, int32_t count, int64_t m, int64_t k,
+                                      void *stream) {
+  clear_error();
+  if (count <= 0 || count > kMaxGroups || ns == nullptr)
+    return fail(NF4S_ERR_INVALID_ARGUMENT, "count must be 1..%d with sizes", kMaxGroups);
+  const int64_t need = fwd_workspace_bytes(ns, count, m, k);
+  if (need > kScratchBytes)
+    return fail(NF4S_ERR_UNSUPPORTED_SHAPE,
+                "split-K workspace of %lld bytes exceeds the static scratch of %lld bytes; "
+                "use nf4s_gemm_fwd_grouped_ws with a workspace of that size",
+                (long long)need, (long long)kScratchBytes);
+  void *p = nullptr;
+  const int32_t rc = scratch_on_current_device(&p);
+  if (rc != NF4S_OK) return rc;
+  return gemm_fwd_groups(x, ws, ns, ys, count, m, k, as_stream(stream), p, kScratchBytes);
 }
 
 int32_t nf4s_gemm_fwd_swiglu(const uint16_t *x, const nf4s_tensor *w_gate,

@@ -224,6 +224,24 @@ int32_t nf4s_gemm_fwd_workspace_size(const int64_t *ns, int32_t count, int64_t m
                                      int64_t k, int64_t *bytes);
 
 /*
+ * nf4s_gemm_fwd_grouped_ws whose split-K workspace is the library's own
+ * static device array (64 MiB per GPU, allocated with the code object and
+ * held until the process ends) instead of a caller buffer: this call
+ * allocates nothing, ever.  No counterpart in the reference: it is for
+ * callers that cannot allocate (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  Fails with
+ * NF4S_ERR_UNSUPPORTED_SHAPE when the split needs more than the array holds
+ * (possible only on devices with more than 256 CUs).  Every call on one GPU
+ * shares that GPU's array: calls that overlap on one GPU (different streams
+ * without ordering, or several host threads) race.  Results are bit-identical
+ * to nf4s_gemm_fwd_grouped_ws with a large enough workspace.
+ */
+int32_t nf4s_gemm_fwd_grouped_noalloc(const uint16_t *x, const nf4s_tensor *ws,
+                                      const int64_t *ns, uint16_t *const *ys,
+                                      int32_t count, int64_t m, int64_t k,
+                                      void *stream);
+
+/*
  * Weight gradient, bf16 in, fp32 out: dw[n, k] = sum_m dy[m, n] * x[m, k]
  * (accumulate = 0), or dw += that sum (accumulate != 0).  Replaces the d_wd,
  * d_wg / d_wu, d_wo and d_wq / d_wk / d_wv loops of single_layer_backward

@@ -143,6 +143,9 @@ extern "C" {
                                     stream: *mut c_void) -> i32;
     pub fn nf4s_gemm_fwd_workspace_size(ns: *const i64, count: i32, m: i64, k: i64,
                                         bytes: *mut i64) -> i32;
+    pub fn nf4s_gemm_fwd_grouped_noalloc(x: *const u16, ws: *const Nf4sTensor, ns: *const i64,
+                                         ys: *const *mut u16, count: i32, m: i64, k: i64,
+                                         stream: *mut c_void) -> i32;
     pub fn nf4s_gemm_wgrad(dy: *const c_void, x: *const c_void, m: i64, n: i64, k: i64,
                            dw: *mut f32, accumulate: i32, stream: *mut c_void) -> i32;
 

@@ -1,0 +1,86 @@
+"""nf4s_gemm_fwd_grouped_noalloc (the split-K forward on the library's static
+per-GPU scratch) against nf4s_gemm_fwd_grouped_ws with a caller workspace,
+both through the C ABI: bit-identical outputs on two calls in a row, the
+second smaller, so stale partials of the first call would show in the second.
+"""
+import ctypes
+
+import pytest
+import torch
+
+from aethelstream_amd import _lib, nf4
+
+pytestmark = pytest.mark.gpu
+
+
+def _weights(shapes, seed):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    return [nf4.quantize_weight(torch.randn(n, k, device="cuda", generator=g) * 0.02,
+                                double_quant=dq) for n, k, dq in shapes]
+
+
+def _args(ws, m):
+    descs = (_lib.Nf4sTensor * len(ws))(*[w.descriptor() for w in ws])
+    ns = (ctypes.c_int64 * len(ws))(*[w.shape[0] for w in ws])
+    outs = [torch.full((m, w.shape[0]), float("nan"), dtype=torch.bfloat16, device="cuda")
+            for w in ws]
+    ys = (ctypes.c_void_p * len(ws))(*[o.data_ptr() for o in outs])
+    return descs, ns, outs, ys
+
+
+def _workspace_bytes(ns, count, m, k):
+    b = ctypes.c_int64()
+    _lib.check(_lib.load().nf4s_gemm_fwd_workspace_size(ns, count, m, k, ctypes.byref(b)))
+    return b.value
+
+
+def _run_pair(ws, m, k, seed):
+    """Returns (noalloc outputs, workspace outputs, workspace bytes)."""
+    lib = _lib.load()
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    x = torch.randn(m, k, device="cuda", generator=g).to(torch.bfloat16)
+    stream = torch.cuda.current_stream().cuda_stream
+    d1, ns, out_na, ys1 = _args(ws, m)
+    print(f"noalloc m={m} k={k} ns={list(ns)}", flush=True)
+    _lib.check(lib.nf4s_gemm_fwd_grouped_noalloc(x.data_ptr(), d1, ns, ys1, len(ws), m, k,
+                                                 stream))
+    d2, ns2, out_ws, ys2 = _args(ws, m)
+    nbytes = _workspace_bytes(ns2, len(ws), m, k)
+    work = torch.empty(max(nbytes, 16), dtype=torch.uint8, device="cuda")
+    _lib.check(lib.nf4s_gemm_fwd_grouped_ws(x.data_ptr(), d2, ns2, ys2, len(ws), m, k,
+                                            work.data_ptr(), nbytes, stream))
+    torch.cuda.synchronize()
+    return out_na, out_ws, nbytes
+
+
+def test_noalloc_equals_workspace_entry_point_twice():
+    # Call 1: 8 output tiles on 256 CUs -> the largest split (64 MiB of
+    # partials at 32 slices).  Call 2: fewer tiles, rows and steps, a ragged
+    # m, and a double-quant + fp32-absmax pair (two launches on the scratch).
+    cases = [
+        (_weights([(640, 8192, True), (384, 8192, True)], 1), 512, 8192),
+        (_weights([(256, 4096, True), (128, 4096, False)], 2), 300, 4096),
+    ]
+    for i, (ws, m, k) in enumerate(cases):
+        a, b, nbytes = _run_pair(ws, m, k, seed=10 + i)
+        assert nbytes > 0, "the case must take the split-K path"
+        for ya, yb in zip(a, b):
+            assert not torch.isnan(ya).any()
+            assert torch.equal(ya, yb), f"call {i}: noalloc output differs"
+
+
+def test_noalloc_without_split_matches_plain_forward():
+    # Whole rounds (no split): the plain grouped forward, bit for bit.
+    lib = _lib.load()
+    ws = _weights([(128 * 256, 512, True)], 3)
+    m, k = 512, 512
+    x = torch.randn(m, k, device="cuda").to(torch.bfloat16)
+    d, ns, out, ys = _args(ws, m)
+    assert _workspace_bytes(ns, 1, m, k) == 0
+    _lib.check(lib.nf4s_gemm_fwd_grouped_noalloc(x.data_ptr(), d, ns, ys, 1, m, k,
+                                                 torch.cuda.current_stream().cuda_stream))
+    d2, ns2, ref, ys2 = _args(ws, m)
+    _lib.check(lib.nf4s_gemm_fwd_grouped(x.data_ptr(), d2, ns2, ys2, 1, m, k,
+                                         torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    assert torch.equal(out[0], ref[0])
