@@ -359,17 +359,15 @@ struct FwdBatchProducer : FwdStore {
 // 4(q ^ c) + (k ^ c), 16 distinct; a 32-lane half of a transposed read
 // covers c = 0..3 at units 4j..4j+3 (fragment j), physical units
 // 4(j ^ c) + (u % 4 ^ c), 16 distinct.
-template <bool kDQ>
-struct DgradProducer : PerStepLoads<kDQ, DgradProducer<kDQ>> {
+// DgradStore holds the thread mapping, the LDS stores and the transposed
+// fragment reads; the two input-gradient producers differ only in how the
+// packed words and absmax reach the registers.
+struct DgradStore {
   static constexpr bool kFwd = false;
-  const uint8_t *ptr;
-  int64_t am_idx;
   uint32_t valid_mask;  // all ones when the thread's columns exist
   int sidx[4];          // LDS unit of the thread's word k
   uint32_t roff[4];     // byte offset of the lane's read of fragment j (rows 0-3 of sub-step 0)
-  AbsmaxRef am;
-  __device__ void init(const GemmArgs &g, int64_t o0, uint32_t b0_lds) {
-    (void)b0_lds;
+  __device__ void init_layout(const GemmArgs &g, int64_t o0) {
     const int r = threadIdx.x >> 2, q = threadIdx.x & 3, c = r & 3;
 #pragma unroll
     for (int k = 0; k < 4; ++k) sidx[k] = 16 * r + 4 * (q ^ c) + (k ^ c);
@@ -379,19 +377,7 @@ struct DgradProducer : PerStepLoads<kDQ, DgradProducer<kDQ>> {
     for (int j = 0; j < 4; ++j)
       roff[j] = (uint32_t)(256 * (8 * (lane >> 5) + cr) + 16 * (4 * (j ^ cr) + (ub ^ cr)) +
                            8 * (l16 & 1));
-    const int64_t col = o0 + 32 * q;
-    const bool valid = col < g.wk;
-    valid_mask = valid ? 0xffffffffu : 0u;
-    const int64_t cc = valid ? col : 0;
-    ptr = g.packed + (int64_t)r * (g.wk >> 1) + (cc >> 1);
-    am_idx = (int64_t)r * (g.wk >> 6) + (cc >> 6);
-    am = g.am;
-  }
-  __device__ __forceinline__ void load_step(const GemmArgs &g, int64_t step, u32x4 &w,
-                                            AbsRaw &a) const {
-    // Step s covers W rows 64s .. 64s+63.
-    w = *reinterpret_cast<const u32x4 *>(ptr + step * 64 * (g.wk >> 1));
-    a = absmax_load<kDQ>(am, am_idx + step * 64 * (g.wk >> 6));
+    valid_mask = (o0 + 32 * q < g.wk) ? 0xffffffffu : 0u;
   }
   // Columns beyond k read column 0's bytes and are zeroed via the absmax.
   __device__ __forceinline__ float masked(float a) const {
@@ -431,6 +417,130 @@ struct DgradProducer : PerStepLoads<kDQ, DgradProducer<kDQ>> {
       word_merge(x, o);
       this->template store<0, k, 0>(lds, o);
     });
+  }
+};
+
+// Input-gradient producer with one packed load, one absmax code and one
+// scale load per step and thread (any n % 64 == 0, k % 64 == 0).
+template <bool kDQ>
+struct DgradProducer : DgradStore, PerStepLoads<kDQ, DgradProducer<kDQ>> {
+  const uint8_t *ptr;
+  int64_t am_idx;
+  AbsmaxRef am;
+  __device__ void init(const GemmArgs &g, int64_t o0, uint32_t b0_lds) {
+    (void)b0_lds;
+    init_layout(g, o0);
+    const int r = threadIdx.x >> 2, q = threadIdx.x & 3;
+    const int64_t col = o0 + 32 * q;
+    const int64_t cc = col < g.wk ? col : 0;
+    ptr = g.packed + (int64_t)r * (g.wk >> 1) + (cc >> 1);
+    am_idx = (int64_t)r * (g.wk >> 6) + (cc >> 6);
+    am = g.am;
+  }
+  __device__ __forceinline__ void load_step(const GemmArgs &g, int64_t step, u32x4 &w,
+                                            AbsRaw &a) const {
+    // Step s covers W rows 64s .. 64s+63.
+    w = *reinterpret_cast<const u32x4 *>(ptr + step * 64 * (g.wk >> 1));
+    a = absmax_load<kDQ>(am, am_idx + step * 64 * (g.wk >> 6));
+  }
+};
+
+// Input-gradient producer with batched absmax loads (k % 128 == 0, n % 256
+// == 0, dq_group >= 2; a 4-step unroll).  A step's absmax is one value per
+// (W row, block), and the thread's blocks of consecutive steps lie 64 rows
+// apart, in different cache lines.  So the four threads of a row (quarters
+// q = 0..3) load the absmax of four different steps: thread (r, q) loads,
+// for step 4g + q, the two blocks' double-quant codes of row r (2 bytes) and
+// their scale (or the two fp32 absmax), one group of four steps ahead.  In
+// step t the absmax of step t + 1 then comes from quad lane (t + 1) % 4 by a
+// DPP broadcast, and the thread keeps its own block's byte.  Two small loads
+// per four steps instead of eight.  The packed words keep the per-step loads
+// (a step's 16 bytes per thread come from one row, the next step's from a
+// row 64 further down).
+template <bool kDQ>
+struct DgradBatchProducer : DgradStore {
+  static constexpr int kUnroll = 4;
+  const uint8_t *ptr;       // packed bytes of (row r, quarter q) at step 0
+  int64_t pstride;          // packed bytes per step (64 W rows)
+  int64_t gblk;             // absmax block (row r + 64q, blocks b0, b0 + 1) of group 0
+  int64_t gstride;          // blocks per group of 4 steps (256 W rows)
+  int64_t ngroups;
+  uint32_t shift;           // 8 * (q >> 1): the thread's block within the pair
+  AbsmaxRef am;
+  u32x4 w[2];
+  u32x4 w0;
+  u32x2 cur, nxt;           // kDQ: {code pair, scale bits}; else {absmax b0, absmax b0 + 1}
+  __device__ void init(const GemmArgs &g, int64_t o0, uint32_t b0_lds) {
+    (void)b0_lds;
+    init_layout(g, o0);
+    const int r = threadIdx.x >> 2, q = threadIdx.x & 3;
+    ptr = g.packed + (int64_t)r * (g.wk >> 1) + ((o0 + 32 * q) >> 1);
+    pstride = 64 * (g.wk >> 1);
+    gblk = (int64_t)(r + 64 * q) * (g.wk >> 6) + (o0 >> 6);
+    gstride = 256 * (g.wk >> 6);
+    ngroups = g.R >> 8;
+    shift = 8u * (uint32_t)(q >> 1);
+    am = g.am;
+  }
+  __device__ __forceinline__ void load_group(int64_t gi, u32x2 &v) const {
+    const int64_t blk = gblk + gi * gstride;
+    if constexpr (kDQ) {
+      v.x = *reinterpret_cast<const uint16_t *>(am.q + blk);
+      v.y = __builtin_bit_cast(uint32_t, am.scale[blk >> am.group_shift]);
+    } else {
+      v = *reinterpret_cast<const u32x2 *>(am.absmax + blk);
+    }
+  }
+  // Element i (step 4g + i) of a group, from quad lane i.  The vector
+  // elements are copied to scalars first (see FwdBatchProducer).
+  template <int i>
+  __device__ __forceinline__ float group_absmax(const u32x2 &v) const {
+    const uint32_t x = v.x, y = v.y;
+    const uint32_t bx = (uint32_t)__builtin_amdgcn_mov_dpp((int)x, i * 0x55, 0xf, 0xf, false);
+    const uint32_t by = (uint32_t)__builtin_amdgcn_mov_dpp((int)y, i * 0x55, 0xf, 0xf, false);
+    if constexpr (kDQ) {
+      return (float)((bx >> shift) & 0xffu) * __builtin_bit_cast(float, by);
+    } else {
+      return __builtin_bit_cast(float, shift != 0u ? by : bx);
+    }
+  }
+  __device__ __forceinline__ void load_words(int64_t step, u32x4 &v) const {
+    v = *reinterpret_cast<const u32x4 *>(ptr + step * pstride);
+  }
+  __device__ __forceinline__ void prologue_load(const GemmArgs &g, int64_t nsteps) {
+    (void)g;
+    load_words(0, w0);
+    load_words(nsteps > 1 ? 1 : 0, w[1]);
+    load_group(0, cur);
+  }
+  __device__ __forceinline__ void prologue_store(u32x4 *lds) const {
+    store_tile(lds, w0, masked(group_absmax<0>(cur)));
+  }
+  template <int kPhase>
+  __device__ __forceinline__ void issue_loads(const GemmArgs &g, int64_t t, int64_t nsteps) {
+    (void)g;
+    const int64_t t2 = (t + 2 < nsteps) ? t + 2 : nsteps - 1;
+    load_words(t2, w[kPhase & 1]);
+    if constexpr (kPhase == 0) {
+      int64_t gi = (t >> 2) + 1;
+      if (gi > ngroups - 1) gi = ngroups - 1;  // look-ahead past the end: unused
+      load_group(gi, nxt);
+    }
+  }
+  template <int kPhase>
+  __device__ __forceinline__ void prepare() {}
+  template <int kPhase>
+  __device__ __forceinline__ uint32_t word(int k) const {
+    return w[(kPhase + 1) & 1][k];
+  }
+  template <int kPhase>
+  __device__ __forceinline__ float table_absmax() const {
+    if constexpr (kPhase == 3) return masked(group_absmax<0>(nxt));
+    else return masked(group_absmax<kPhase + 1>(cur));
+  }
+  template <int kPhase>
+  __device__ __forceinline__ void finish() {
+    if constexpr (kPhase == 3) cur = nxt;
   }
 };
 
@@ -1533,6 +1643,20 @@ static int32_t gemm_dgrad_groups(const uint16_t *const *dys, const nf4s_tensor *
     q.lda = ns[i];
     ga.grp[ga.ngroups++] = q;
   }
+  // Batched absmax loads: whole 4-step groups for every weight, both blocks
+  // of a 128-column tile in every row (k % 128), aligned pair loads, and
+  // the two blocks of a pair inside one double-quant scale group.
+  bool batch = k % 128 == 0;
+  for (int32_t i = 0; i < count && batch; ++i) {
+    batch = ns[i] % 256 == 0;
+    if (dq)
+      batch = batch && aligned(ws[i].absmax_q, 2) && ws[i].dq_group >= 2;
+    else
+      batch = batch && aligned(ws[i].absmax, 8);
+  }
+  if (batch)
+    return dq ? launch_dgrad<DgradBatchProducer<true>>(ga, s)
+              : launch_dgrad<DgradBatchProducer<false>>(ga, s);
   return dq ? launch_dgrad<DgradProducer<true>>(ga, s) : launch_dgrad<DgradProducer<false>>(ga, s);
 }
 

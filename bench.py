@@ -156,22 +156,63 @@ def read_traffic():
     return None
 
 
-def cpu_baseline_dequant(ws, budget_s):
+class pinned_core:
+    """Pins the calling thread (the bench's main thread, which runs the oracle)
+    to one core for the CPU legs and restores its mask afterwards, in-process:
+    the GPU process never re-executes itself.  The reference path is
+    single-threaded (shard_engine and doublepass start no threads)."""
+
+    def __enter__(self):
+        self.prev = os.sched_getaffinity(0)
+        self.core = min(self.prev)
+        os.sched_setaffinity(0, {self.core})
+        return self
+
+    def __exit__(self, *exc):
+        os.sched_setaffinity(0, self.prev)
+
+
+def host_facts() -> dict:
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    model = ln.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model, "nproc": os.cpu_count(),
+            "allowed_cores": len(os.sched_getaffinity(0))}
+
+
+def algorithmic_bytes_fp32_absmax(shapes, bs=64) -> int:
+    """The reference's own format (fp32 absmax, nf4.rs:37-83): 0.5 + 4/64 + 2
+    bytes per element with f16 out."""
+    total = 0
+    for _, r, c in shapes:
+        n = r * c
+        total += n // 2 + 4 * ((n + bs - 1) // bs) + 2 * n
+    return total
+
+
+def cpu_baseline_dequant(ws, budget_s, core):
     """The oracle's dequant (scalar C restatement of shard_engine/src/nf4.rs:37-83,
-    f16 out as the reference) on the host, single thread, on a bounded sample:
-    whole matrices of the same layer until ~budget_s of CPU time."""
+    fp32 absmax in and f16 out, as the reference) on one pinned core, over
+    whole matrices of the same layer until ~budget_s of CPU time.  The layer's
+    double-quantized absmax is decoded to fp32 outside the timed region: the
+    reference's format has fp32 absmax and no decode."""
     import oracle
     done_bytes, elapsed, mats, i = 0, 0.0, 0, 0
     while elapsed < budget_s and mats < 64:
         w = ws[i % len(ws)]
         pk = w.packed.cpu().numpy()
-        q = w.absmax_q.cpu().numpy()
-        sc = w.absmax_scale.cpu().numpy()
+        am = oracle.dq_decode(w.absmax_q.cpu().numpy(), w.absmax_scale.cpu().numpy(),
+                              w.dq_group)
         t0 = time.perf_counter()
-        am = oracle.dq_decode(q, sc, w.dq_group)
         oracle.dequant_f16(pk, am, w.numel, w.block_size)
         elapsed += time.perf_counter() - t0
-        done_bytes += algorithmic_bytes_dq([("", w.shape[0], w.shape[1])])
+        done_bytes += algorithmic_bytes_fp32_absmax([("", w.shape[0], w.shape[1])])
         mats += 1
         i += 1
     return {
@@ -179,25 +220,78 @@ def cpu_baseline_dequant(ws, budget_s):
         "unit": "GB/s",
         "cores": 1,
         "kind": "port",
-        "sample": f"{mats} whole matrices of the same 7B layer ({done_bytes} algorithmic bytes, "
-                  f"{elapsed:.1f} s): oracle double-quant decode + f16 dequant, 1 thread",
+        "sample": f"{mats} whole matrices of the same 7B layer in the reference's fp32-absmax "
+                  f"format ({done_bytes} algorithmic bytes at 2.5625 B/element, "
+                  f"{elapsed:.1f} s): oracle f16 dequant, 1 thread pinned to core {core}",
     }
 
 
-def cpu_baseline_gemm(rows=8):
-    """The oracle's matmul_tb (doublepass/src/math.rs:9-21, fp32 triple loop,
-    1 thread) on a `rows`-row slice of the 7B gate GEMM; cost is linear in M."""
-    import numpy as np
+def cpu_baseline_quantize(core):
+    """Config 1 on the CPU: the oracle's quantize_nf4 (restatement of
+    shard_engine/python/pipeline/quantizer.py:21-53) of one fp32 4096 x 4096
+    ~ N(0, 0.02) matrix, one pinned core.  Returns the leg and its outputs
+    (the device run is checked against them)."""
     import oracle
-    n, k = 11008, 4096
-    a = oracle.gen_normal(11, rows * k, 1.0).reshape(rows, k)
-    b = oracle.gen_normal(12, n * k, 0.02).reshape(n, k)
+    x = oracle.gen_normal(1, 4096 * 4096, 0.02)
     t0 = time.perf_counter()
-    oracle.matmul_tb(a, b)
+    pk, am = oracle.quantize_nf4(x)
     dt = time.perf_counter() - t0
-    fl = 2.0 * rows * n * k
-    return {"value": round(fl / dt / 1e12, 6), "unit": "TFLOP/s", "cores": 1, "kind": "port",
-            "sample": f"{rows} rows x gate 11008x4096 ({dt:.2f} s); time scales linearly in M"}
+    leg = {"value": round(x.nbytes / dt / 1e6, 2), "unit": "MB/s of fp32 input", "cores": 1,
+           "kind": "port", "sample": f"config 1: one 4096x4096 fp32 matrix ({dt:.2f} s), "
+                                     f"core {core}"}
+    return leg, x, pk, am
+
+
+def cpu_baseline_gemm(core, rows=8):
+    """The oracle's matmul_tb (doublepass/src/math.rs:9-21) and its dY.W loop
+    (doublepass/src/backward.rs:79-85), fp32, one pinned core, on `rows`-row
+    slices of the 7B down projection; cost is linear in the row count."""
+    import oracle
+    d, ff = 4096, 11008
+    w = oracle.gen_normal(12, d * ff, 0.02).reshape(d, ff)        # Wd [d, ff]
+    h = oracle.gen_normal(11, rows * ff, 1.0).reshape(rows, ff)    # hidden [rows, ff]
+    dy = oracle.gen_normal(13, rows * d, 1.0).reshape(rows, d)     # dY [rows, d]
+    t0 = time.perf_counter()
+    oracle.matmul_tb(h, w)                    # [rows, d] = hidden . Wd^T
+    t1 = time.perf_counter()
+    oracle.dgrad(dy, w)                       # [rows, ff] = dY . Wd
+    t2 = time.perf_counter()
+    fl = 2.0 * rows * d * ff
+    return {
+        "fwd": {"value": round(fl / (t1 - t0) / 1e12, 6), "unit": "TFLOP/s", "cores": 1,
+                "kind": "port", "sample": f"{rows} rows of the 7B down forward, hidden . Wd^T "
+                f"({t1 - t0:.2f} s, core {core}); time scales linearly in M"},
+        "dgrad": {"value": round(fl / (t2 - t1) / 1e12, 6), "unit": "TFLOP/s", "cores": 1,
+                  "kind": "port", "sample": f"{rows} rows of d_hidden = dY . Wd "
+                  f"(backward.rs:79-85, {t2 - t1:.2f} s, core {core}); linear in M"},
+    }
+
+
+def bench_quantize_config1(torch, nf4, x, pk_ref, am_ref, args):
+    """Config 1 on the device: nf4s_quantize of the same fp32 4096 x 4096
+    matrix the CPU leg quantized (inputs resident), codes and absmax compared
+    with the oracle's bit for bit."""
+    import numpy as np
+    from aethelstream_amd import _lib
+    import ctypes
+    xd = torch.from_numpy(x).cuda()
+    n = xd.numel()
+    packed = torch.empty((n + 1) // 2, dtype=torch.uint8, device="cuda")
+    absmax = torch.empty((n + 63) // 64, dtype=torch.float32, device="cuda")
+    lib = _lib.load()
+
+    def run():
+        _lib.check(lib.nf4s_quantize(xd.data_ptr(), n, 64, packed.data_ptr(),
+                                     absmax.data_ptr(), torch.cuda.current_stream().cuda_stream))
+
+    ms = timed(torch, run, args.steps, args.warmup, name="config1_quantize")
+    torch.cuda.synchronize()
+    exact = bool(np.array_equal(packed.cpu().numpy(), pk_ref) and
+                 np.array_equal(absmax.cpu().numpy().view(np.uint32), am_ref.view(np.uint32)))
+    moved = 4 * n + packed.numel() + 4 * absmax.numel()
+    return {"ms": round(ms, 5), "input_gbs": round(4 * n / (ms * 1e-3) / 1e9, 2),
+            "bytes_moved_gbs": round(moved / (ms * 1e-3) / 1e9, 2),
+            "codes_absmax_bit_exact_vs_oracle": exact}
 
 
 def bench_dequant(torch, nf4, args):
@@ -503,7 +597,9 @@ def bf16_gemm_reference(torch, dequant_gbs, layer_ms):
         deq_ms = algorithmic_bytes_dq(LAYER_70B) / (dequant_gbs * 1e9) * 1e3
         unfused_ms = 3 * (deq_ms + fl_pass / (tf * 1e12) * 1e3)
         res["unfused_config4_tflops"] = round(3 * fl_pass / (unfused_ms * 1e-3) / 1e12, 1)
-        res["fused_over_unfused"] = round(unfused_ms / layer_ms, 3)
+        # unfused time / fused time: above 1 the fused kernels are faster,
+        # below 1 dequantize-then-hipBLASLt would be.
+        res["fused_speedup_over_unfused"] = round(unfused_ms / layer_ms, 3)
     return res
 
 
@@ -580,10 +676,17 @@ def main():
         except Exception as e:  # reported, the rest of the line still prints
             line["stream"] = {"error": repr(e)}
     if not args.no_cpu_baseline and ws is not None:
-        log("cpu baseline (oracle, 1 thread)")
-        line["cpu_baseline"] = cpu_baseline_dequant(ws, args.cpu_seconds)
+        log("cpu baseline (oracle, 1 pinned core)")
+        with pinned_core() as pc:
+            line["cpu_baseline"] = cpu_baseline_dequant(ws, args.cpu_seconds, pc.core)
+            legs = {"host": host_facts()}
+            if args.workload == "all":
+                legs["quantize_config1"], x1, pk1, am1 = cpu_baseline_quantize(pc.core)
+                legs.update(cpu_baseline_gemm(pc.core))
+        line["cpu_baseline_legs"] = legs
         if args.workload == "all":
-            line["cpu_baseline_gemm"] = cpu_baseline_gemm()
+            log("config 1: device quantize")
+            line["quantize_config1"] = bench_quantize_config1(torch, nf4, x1, pk1, am1, args)
     print(json.dumps(line), flush=True)
 
 

@@ -118,6 +118,30 @@ def test_fwd_batched_equals_per_step(m, n, k, dq):
     assert torch.equal(y_batched.view(torch.int16), y_step.view(torch.int16))
 
 
+@pytest.mark.parametrize("m,n,k", [(700, 256, 128), (513, 512, 1024), (1024, 1024, 384)])
+@pytest.mark.parametrize("dq_group", [0, 2, 256])
+def test_dgrad_batched_equals_per_step(m, n, k, dq_group):
+    # The input gradient's batched absmax loads (n % 256, k % 128) against the
+    # per-step loads, selected by moving the absmax (or its codes) off the
+    # alignment the pair loads need: same products, same reduction order,
+    # bit-identical outputs.  dq_group 2: each scale covers exactly a pair.
+    dq = dq_group > 0
+    w32 = oracle.gen_normal(43 + n + k, n * k, 0.02)
+    w = nf4.quantize_weight(torch.from_numpy(w32).to(DEV).view(n, k), double_quant=dq,
+                            dq_group=dq_group or nf4.DQ_GROUP)
+    dy, _ = _act(m, n, 11 + m)
+    dx_batched = gemm.linear_dgrad(dy, w)
+    if dq:
+        w2 = nf4.Nf4Weight(packed=w.packed, absmax=None, shape=w.shape,
+                           absmax_q=_misaligned(w.absmax_q, 1), absmax_scale=w.absmax_scale,
+                           dq_group=w.dq_group)
+    else:
+        w2 = nf4.Nf4Weight(packed=w.packed, absmax=_misaligned(w.absmax, 1), shape=w.shape)
+    dx_step = gemm.linear_dgrad(dy, w2)
+    torch.cuda.synchronize()
+    assert torch.equal(dx_batched.view(torch.int16), dx_step.view(torch.int16))
+
+
 @pytest.mark.parametrize("m,n,k", [(1, 64, 128), (64, 128, 64), (512, 128, 128),
                                    (700, 320, 300 - 300 % 64 + 64), (513, 256, 320)])
 @pytest.mark.parametrize("dq", [False, True])
@@ -225,7 +249,8 @@ def test_fwd_grouped_equals_separate(m, k, ns, dqs):
 
 
 @pytest.mark.parametrize("m,k,ns", [(700, 192, [128, 64, 64]), (513, 256, [320, 128]),
-                                    (64, 128, [64]), (1024, 512, [256, 64, 64, 128])])
+                                    (64, 128, [64]), (1024, 512, [256, 64, 64, 128]),
+                                    (640, 256, [256, 512])])
 @pytest.mark.parametrize("dq", [False, True])
 def test_dgrad_sum_small_vs_oracle(m, k, ns, dq):
     ws = [_weight(n, k, 61 + i * 5 + n, dq) for i, n in enumerate(ns)]
