@@ -439,6 +439,26 @@ def bench_gemm(torch, nf4, gemm, args):
                   name="gate_up_grouped")
     ms_sw = timed(torch, lambda: gemm.linear_swiglu(h, ws[4], ws[5], hsw), steps4, 1,
                   name="gate_up_swiglu")
+    # RMSNorm before q/k/v and before gate/up (forward.rs:173, 249), run
+    # unfused: its time bounds what fusing it into the GEMM could save.
+    from aethelstream_amd import norm
+    xr = torch.randn(M, 8192, device="cuda", generator=g)
+    wr = 1.0 + 0.1 * torch.randn(8192, device="cuda", generator=g)
+    hr = torch.empty(M, 8192, dtype=torch.bfloat16, device="cuda")
+    rr = torch.empty(M, dtype=torch.float32, device="cuda")
+    ms_rn = timed(torch, lambda: norm.rms_norm_fwd(xr, wr, out=hr, rms=rr), args.steps, 1,
+                  name="rmsnorm_70b")
+
+    def fwd_pass_with_norms():
+        norm.rms_norm_fwd(xr, wr, out=hr, rms=rr)
+        gemm.linear_fwd_grouped(hr, ws[0:3], ys[0:3])
+        gemm.linear_fwd(h, ws[3], ys[3])
+        norm.rms_norm_fwd(xr, wr, out=hr, rms=rr)
+        gemm.linear_fwd_grouped(hr, ws[4:6], ys[4:6])
+        gemm.linear_fwd(hid, ws[6], ys[6])
+
+    ms_fn = timed(torch, fwd_pass_with_norms, steps4, 1, name="config4_fwd_pass_with_rmsnorm")
+    del xr, hr
     tf_l = 3 * fl_pass / (ms_l * 1e-3) / 1e12
     res["config4_70b_layer"] = {
         "tflops": round(tf_l, 1), "ms_per_layer_step": round(ms_l, 3),
@@ -453,6 +473,14 @@ def bench_gemm(torch, nf4, gemm, args):
         "dgrad_pass_tflops": round(fl_pass / (ms_d * 1e-3) / 1e12, 1),
         "wgrad_pass_tflops": round(fl_pass / (ms_w * 1e-3) / 1e12, 1),
         "per_matrix": per,
+        "rmsnorm": {
+            "op": "nf4s_rmsnorm_fwd, x fp32 [8192, 8192] -> bf16, unfused",
+            "us": round(ms_rn * 1e3, 2),
+            "gbs": round(6 * M * 8192 / (ms_rn * 1e-3) / 1e9, 1),
+            "fwd_pass_ms": round(ms_f, 3),
+            "fwd_pass_with_two_rmsnorms_ms": round(ms_fn, 3),
+            "share_of_fwd_pass": round((ms_fn - ms_f) / ms_fn, 4),
+        },
     }
     return res
 

@@ -255,6 +255,19 @@ int32_t nf4s_gemm_fwd_grouped_noalloc(const uint16_t *x, const nf4s_tensor *ws,
 int32_t nf4s_gemm_wgrad(const void *dy, const void *x, int64_t m, int64_t n,
                         int64_t k, float *dw, int32_t accumulate, void *stream);
 
+/*
+ * RMSNorm forward producing the fused GEMMs' bf16 operand: for each row b of
+ * x [m, d] (fp32), rms[b] = sqrt(sum_i x[b,i]^2 / d + eps) and y[b,i] =
+ * bf16((x[b,i] / rms[b]) * w[i]), fp32 arithmetic with correctly rounded
+ * division and square root.  Replaces rms_norm_fwd
+ * (doublepass/src/math.rs:28-59) at forward.rs:173 and :249, whose outputs
+ * feed the q/k/v and gate/up GEMMs; rms (fp32, m values) is kept for the
+ * backward.  The squares are summed as a tree, not in index order.
+ * Requires d % 4 == 0, d <= 32768, x and w 16-byte aligned, y 8-byte aligned.
+ */
+int32_t nf4s_rmsnorm_fwd(const float *x, const float *w, int64_t m, int64_t d, float eps,
+                         uint16_t *y, float *rms, void *stream);
+
 /* ---------------------------------------------------------------------------
  * Streamed layer stack (one GPU).  Layers wait in pinned host memory and are
  * copied into a two-slot device double buffer on a dedicated copy stream.

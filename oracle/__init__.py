@@ -57,6 +57,7 @@ def lib():
         L.or_matmul_tb.argtypes = [P, P, i64, i64, i64, P]
         L.or_dgrad.argtypes = [P, P, i64, i64, i64, P]
         L.or_wgrad.argtypes = [P, P, i64, i64, i64, P]
+        L.or_rmsnorm_fwd.argtypes = [P, P, i64, i64, ctypes.c_float, P, P, P]
         L.or_gen_normal.argtypes = [ctypes.c_uint64, i64, ctypes.c_double, P]
         _lib = L
     return _lib
@@ -163,6 +164,18 @@ def wgrad(dy: np.ndarray, x: np.ndarray, dw: np.ndarray = None) -> np.ndarray:
     out = np.zeros((n, k), np.float32) if dw is None else np.array(dw, np.float32, copy=True)
     lib().or_wgrad(_p(dy), _p(x), m, n, k, _p(out))
     return out
+
+
+def rmsnorm_fwd(x: np.ndarray, w: np.ndarray, eps: float = 1e-6):
+    """math.rs:36-59: returns (y, x_hat, rms) in fp32."""
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    m, d = x.shape
+    y = np.zeros((m, d), np.float32)
+    xh = np.zeros((m, d), np.float32)
+    rms = np.zeros(m, np.float32)
+    lib().or_rmsnorm_fwd(_p(x), _p(w), m, d, eps, _p(y), _p(xh), _p(rms))
+    return y, xh, rms
 
 
 def bf16_bits_to_f32(bits: np.ndarray) -> np.ndarray:

@@ -266,6 +266,28 @@ void or_dgrad(const float *dy, const float *w, int64_t m, int64_t n,
         }
 }
 
+/* doublepass/src/math.rs:36-59: the sum of squares in index order, one fp32
+ * division by d, sqrt(mean_sq + eps), then x / rms and * w per element. */
+void or_rmsnorm_fwd(const float *x, const float *w, int64_t m, int64_t d, float eps,
+                    float *y, float *x_hat, float *rms) {
+    for (int64_t b = 0; b < m; ++b) {
+        float s = 0.0f;
+        for (int64_t i = 0; i < d; ++i) {
+            const float v = x[b * d + i];
+            const float sq = v * v;
+            s += sq;
+        }
+        const float mean_sq = s / (float)d;
+        const float r = sqrtf(mean_sq + eps);
+        rms[b] = r;
+        for (int64_t i = 0; i < d; ++i) {
+            const float xh = x[b * d + i] / r;
+            x_hat[b * d + i] = xh;
+            y[b * d + i] = xh * w[i];
+        }
+    }
+}
+
 static inline uint64_t splitmix64(uint64_t *s) {
     uint64_t z = (*s += 0x9e3779b97f4a7c15ull);
     z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;

@@ -26,6 +26,9 @@
  *   or_dgrad             closed form vs fp64 numpy on small shapes
  *   or_wgrad             closed form vs fp64 numpy on small shapes; exact on
  *                        small-integer data
+ *   or_rmsnorm_fwd       closed form vs fp64 numpy; exact special cases (a
+ *                        zero row gives rms = sqrt(eps) and y = 0; a row of
+ *                        equal values v gives x_hat = v / sqrt(v^2 + eps))
  */
 #ifndef NF4_ORACLE_H
 #define NF4_ORACLE_H
@@ -104,6 +107,12 @@ void or_dgrad(const float *dy, const float *w, int64_t m, int64_t n,
  * dw must be zeroed by the caller for a fresh result. */
 void or_wgrad(const float *dy, const float *x, int64_t m, int64_t n,
               int64_t k, float *dw);
+
+/* rms_norm_fwd (doublepass/src/math.rs:28-59): per row b of x [m, d],
+ * mean_sq = (sum_i x^2) / d summed in index order, rms[b] = sqrt(mean_sq +
+ * eps), x_hat = x / rms[b], y = x_hat * w[i]; fp32 throughout. */
+void or_rmsnorm_fwd(const float *x, const float *w, int64_t m, int64_t d, float eps,
+                    float *y, float *x_hat, float *rms);
 
 /* Deterministic input generator: splitmix64(seed) -> 53-bit uniform ->
  * Box-Muller in fp64 -> * sigma -> fp32 round to nearest. */

@@ -148,6 +148,8 @@ extern "C" {
                                          stream: *mut c_void) -> i32;
     pub fn nf4s_gemm_wgrad(dy: *const c_void, x: *const c_void, m: i64, n: i64, k: i64,
                            dw: *mut f32, accumulate: i32, stream: *mut c_void) -> i32;
+    pub fn nf4s_rmsnorm_fwd(x: *const f32, w: *const f32, m: i64, d: i64, eps: f32, y: *mut u16,
+                            rms: *mut f32, stream: *mut c_void) -> i32;
 
     pub fn nf4s_host_alloc(bytes: i64, out: *mut *mut c_void) -> i32;
     pub fn nf4s_host_free(p: *mut c_void) -> i32;

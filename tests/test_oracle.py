@@ -246,3 +246,28 @@ def test_generator_statistics():
     assert abs(float(x.mean())) < 2e-4
     assert abs(float(x.std()) - 0.02) < 2e-4
     assert np.array_equal(x, oracle.gen_normal(42, 1 << 18, 0.02))
+
+
+def test_rmsnorm_against_fp64_and_special_rows():
+    """or_rmsnorm_fwd (math.rs:36-59) on a non-square shape against the fp64
+    closed form; a zero row (rms = sqrt(eps), y = 0) and a row of equal
+    values (x_hat = v / sqrt(v^2 + eps)) pin the eps placement and the
+    division; a varying w catches a w indexed by row instead of column."""
+    rng = np.random.default_rng(7)
+    m, d = 5, 96
+    x = rng.standard_normal((m, d)).astype(np.float32)
+    x[3] = 0.0
+    x[4] = np.float32(0.25)
+    w = (1.0 + np.arange(d, dtype=np.float32) / d).astype(np.float32)
+    eps = 1e-6
+    y, xh, rms = oracle.rmsnorm_fwd(x, w, eps)
+    x64 = x.astype(np.float64)
+    r64 = np.sqrt((x64 ** 2).mean(axis=1) + eps)
+    np.testing.assert_allclose(rms, r64, rtol=1e-6)
+    np.testing.assert_allclose(xh, x64 / r64[:, None], rtol=1e-6, atol=1e-7)
+    np.testing.assert_allclose(y, x64 / r64[:, None] * w.astype(np.float64)[None, :],
+                               rtol=2e-6, atol=1e-7)
+    assert rms[3] == np.float32(np.sqrt(np.float32(eps))) and not y[3].any()
+    want = np.float32(0.25) / np.sqrt(np.float32(0.0625) + np.float32(eps))
+    assert np.all(xh[4] == want)
+    np.testing.assert_array_equal(y[4], xh[4] * w)
