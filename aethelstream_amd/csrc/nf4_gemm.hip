@@ -574,8 +574,9 @@ __device__ __forceinline__ void read_frag(const Producer &prod, const u32x4 *__r
 //      'n' is R plus an N job
 //   M  one quarter of the product table (4 products, 2 conversions, the
 //      quarter's two low/high byte words)
-//   W  one lookup stage of a packed word, in order: selectors, masks, even
-//      elements, odd elements, pairs, then natural order and the 16-B store
+//   W  one lookup stage of a packed word (NatLookup), in order: selectors,
+//      plane controls, elements 0-3, elements 4-7, the bf16 pairs, the
+//      16-B store
 //   N  one activation DMA of the NEXT step's tile, rows 64-127, into the
 //      other buffer
 //   A  one activation DMA of the step after next (t+2), rows 0-63, into the
@@ -674,8 +675,8 @@ __device__ __forceinline__ void gemm_step(const GemmArgs &g, Producer &prod,
   const int64_t t2 = (t + 2 < nsteps) ? t + 2 : nsteps - 1;
   Lut16 lut;
   uint32_t lutd[2];
-  WordLookup wl;
-  uint32_t wp[4][4];  // word_pairs output of each packed word
+  NatLookup wl;
+  uint32_t wp[4][4];  // dequantized elements of each packed word, memory order
   float ta = 0.0f;
   auto dma = [&](u32x4 *dst, int d, int64_t step) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(arsrc, (lds_void_t *)(dst + d * 64), 16,
@@ -728,19 +729,17 @@ __device__ __forceinline__ void gemm_step(const GemmArgs &g, Producer &prod,
       constexpr int j = plan_index(kFwd ? kPlanFwd : kPlanDgrad, n, 'W');
       constexpr int k = j / kWordStages, stage = j % kWordStages;
       if constexpr (stage == 0) {
-        word_select_idx(prod.template word<kPhase>(k), wl);
+        nat_select(prod.template word<kPhase>(k), wl);
       } else if constexpr (stage == 1) {
-        word_select_mask(prod.template word<kPhase>(k), wl);
+        nat_controls(wl);
       } else if constexpr (stage == 2) {
-        word_even(lut, wl);
+        nat_planes_a(lut, wl);
       } else if constexpr (stage == 3) {
-        word_odd(lut, wl);
+        nat_planes_b(lut, wl);
       } else if constexpr (stage == 4) {
-        word_pairs(wl, wp[k]);
+        nat_merge(wl, wp[k]);
       } else {
-        uint32_t o[4];
-        pairs_merge(wp[k], o);
-        prod.template store<kPar, k, 0>(Bnext, o);
+        prod.template store<kPar, k, 0>(Bnext, wp[k]);
       }
     }
     __builtin_amdgcn_sched_barrier(0);

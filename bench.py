@@ -439,6 +439,35 @@ def bench_gemm(torch, nf4, gemm, args):
                   name="gate_up_grouped")
     ms_sw = timed(torch, lambda: gemm.linear_swiglu(h, ws[4], ws[5], hsw), steps4, 1,
                   name="gate_up_swiglu")
+    # The unfused alternative, measured end to end: each pass dequantizes the
+    # layer's 7 weights to bf16 (one grouped launch), then runs the same
+    # products as plain bf16 GEMMs in torch (hipBLASLt): x . W^T forward,
+    # dY . W input gradient with the sums accumulated by addmm.
+    wbf = [torch.empty(w.shape, dtype=torch.bfloat16, device="cuda") for w in ws]
+
+    def unfused_fwd_pass():
+        nf4.dequant_batch(ws, wbf)
+        for a, wb, y in zip(ins, wbf, ys):
+            torch.matmul(a, wb.t(), out=y)
+
+    def unfused_dgrad_pass():
+        nf4.dequant_batch(ws, wbf)
+        torch.matmul(dys[0], wbf[0], out=dxs[0])
+        dxs[0].addmm_(dys[1], wbf[1])
+        dxs[0].addmm_(dys[2], wbf[2])
+        torch.matmul(dys[3], wbf[3], out=dxs[3])
+        torch.matmul(dys[4], wbf[4], out=dxs[4])
+        dxs[4].addmm_(dys[5], wbf[5])
+        torch.matmul(dys[6], wbf[6], out=dxs[6])
+
+    def unfused_layer_step():
+        unfused_fwd_pass()
+        unfused_fwd_pass()
+        unfused_dgrad_pass()
+
+    ms_u = timed(torch, unfused_layer_step, steps4, 1, name="config4_unfused_layer_step")
+    ms_uf = timed(torch, unfused_fwd_pass, steps4, 1, name="config4_unfused_fwd_pass")
+    del wbf
     # RMSNorm before q/k/v and before gate/up (forward.rs:173, 249), run
     # unfused: its time bounds what fusing it into the GEMM could save.
     from aethelstream_amd import norm
@@ -473,6 +502,14 @@ def bench_gemm(torch, nf4, gemm, args):
         "dgrad_pass_tflops": round(fl_pass / (ms_d * 1e-3) / 1e12, 1),
         "wgrad_pass_tflops": round(fl_pass / (ms_w * 1e-3) / 1e12, 1),
         "per_matrix": per,
+        "unfused_measured": {
+            "op": "per pass: nf4s_dequant_batch_bf16 of the 7 weights, then torch.matmul / "
+                  "addmm in bf16 (hipBLASLt)",
+            "tflops": round(3 * fl_pass / (ms_u * 1e-3) / 1e12, 1),
+            "ms_per_layer_step": round(ms_u, 3),
+            "fwd_pass_tflops": round(fl_pass / (ms_uf * 1e-3) / 1e12, 1),
+            "fused_speedup": round(ms_u / ms_l, 3),
+        },
         "rmsnorm": {
             "op": "nf4s_rmsnorm_fwd, x fp32 [8192, 8192] -> bf16, unfused",
             "us": round(ms_rn * 1e3, 2),
@@ -705,9 +742,9 @@ def main():
             line["stream"] = {"error": repr(e)}
     if not args.no_cpu_baseline and ws is not None:
         log("cpu baseline (oracle, 1 pinned core)")
+        legs = {"host": host_facts()}
         with pinned_core() as pc:
             line["cpu_baseline"] = cpu_baseline_dequant(ws, args.cpu_seconds, pc.core)
-            legs = {"host": host_facts()}
             if args.workload == "all":
                 legs["quantize_config1"], x1, pk1, am1 = cpu_baseline_quantize(pc.core)
                 legs.update(cpu_baseline_gemm(pc.core))
