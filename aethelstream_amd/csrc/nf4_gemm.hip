@@ -119,14 +119,14 @@ struct PerStepLoads {
   AbsRaw a[2];
   u32x4 w0;  // step 0 (prologue)
   AbsRaw a0;
-  __device__ __forceinline__ void prologue_load(const GemmArgs &g, int64_t nsteps) {
+  __device__ __forceinline__ void prologue_load(const GemmArgs &g, int nsteps) {
     const Derived &d = static_cast<const Derived &>(*this);
     d.load_step(g, 0, w0, a0);
     d.load_step(g, nsteps > 1 ? 1 : 0, w[1], a[1]);
   }
   template <int kPhase>
-  __device__ __forceinline__ void issue_loads(const GemmArgs &g, int64_t t, int64_t nsteps) {
-    const int64_t t2 = (t + 2 < nsteps) ? t + 2 : nsteps - 1;
+  __device__ __forceinline__ void issue_loads(const GemmArgs &g, int t, int nsteps) {
+    const int t2 = (t + 2 < nsteps) ? t + 2 : nsteps - 1;
     static_cast<const Derived &>(*this).load_step(g, t2, w[kPhase & 1], a[kPhase & 1]);
   }
   template <int kPhase>
@@ -207,10 +207,10 @@ struct FwdProducer : FwdStore, PerStepLoads<kDQ, FwdProducer<kDQ>> {
     am_idx = n * (g.wk >> 6) + g.k0;
     am = g.am;
   }
-  __device__ __forceinline__ void load_step(const GemmArgs &g, int64_t step, u32x4 &w,
+  __device__ __forceinline__ void load_step(const GemmArgs &g, int step, u32x4 &w,
                                             AbsRaw &a) const {
     (void)g;
-    w = *reinterpret_cast<const u32x4 *>(ptr + step * 32);
+    w = *reinterpret_cast<const u32x4 *>(ptr + (int64_t)step * 32);
     a = absmax_load<kDQ>(am, am_idx + step);
   }
 };
@@ -235,7 +235,7 @@ struct FwdBatchProducer : FwdStore {
   static constexpr int kUnroll = 4;
   const uint8_t *pkx, *pky;  // pair loads of instructions X and Y at pair 0
   int64_t am_idx;            // absmax block index of (row) at step 0
-  int64_t npairs, ngroups;
+  int npairs, ngroups;
   u32x4 X[2], Y[2];
   typedef typename std::conditional<kDQ, u32x2, u32x4>::type Group;
   Group cur, nxt;  // kDQ: {codes of 4 blocks, scale bits}; else 4 fp32 absmax
@@ -256,16 +256,16 @@ struct FwdBatchProducer : FwdStore {
     if (ny >= g.wn) ny = g.wn - 1;
     pkx = g.packed + nx * (g.wk >> 1) + 16 * (lane >> 4) + 32 * g.k0;
     pky = g.packed + ny * (g.wk >> 1) + 16 * (lane >> 4) + 32 * g.k0;
-    npairs = g.R >> 7;
-    ngroups = g.R >> 8;
+    npairs = (int)(g.R >> 7);
+    ngroups = (int)(g.R >> 8);
   }
-  __device__ __forceinline__ void load_pair(int64_t p, u32x4 &x, u32x4 &y) const {
-    x = *reinterpret_cast<const u32x4 *>(pkx + p * 64);
-    y = *reinterpret_cast<const u32x4 *>(pky + p * 64);
+  __device__ __forceinline__ void load_pair(int p, u32x4 &x, u32x4 &y) const {
+    x = *reinterpret_cast<const u32x4 *>(pkx + (int64_t)p * 64);
+    y = *reinterpret_cast<const u32x4 *>(pky + (int64_t)p * 64);
   }
-  __device__ __forceinline__ void load_group(const GemmArgs &g, int64_t gi, Group &v) const {
+  __device__ __forceinline__ void load_group(const GemmArgs &g, int gi, Group &v) const {
     (void)g;
-    const int64_t blk = am_idx + 4 * gi;
+    const int64_t blk = am_idx + 4 * (int64_t)gi;
     if constexpr (kDQ) {
       v.x = *reinterpret_cast<const uint32_t *>(am.q + blk);
       v.y = __builtin_bit_cast(uint32_t, am.scale[blk >> am.group_shift]);
@@ -293,7 +293,7 @@ struct FwdBatchProducer : FwdStore {
       y[i] = r[1];
     });
   }
-  __device__ __forceinline__ void prologue_load(const GemmArgs &g, int64_t nsteps) {
+  __device__ __forceinline__ void prologue_load(const GemmArgs &g, int nsteps) {
     (void)nsteps;
     load_pair(0, X[1], Y[1]);
     load_group(g, 0, cur);
@@ -303,15 +303,15 @@ struct FwdBatchProducer : FwdStore {
     store_tile(lds, X[1], group_absmax<0>(cur));
   }
   template <int kPhase>
-  __device__ __forceinline__ void issue_loads(const GemmArgs &g, int64_t t, int64_t nsteps) {
+  __device__ __forceinline__ void issue_loads(const GemmArgs &g, int t, int nsteps) {
     (void)nsteps;
     if constexpr (kPhase == 0 || kPhase == 2) {
-      int64_t p = (t + 2) >> 1;
+      int p = (t + 2) >> 1;
       if (p > npairs - 1) p = npairs - 1;  // look-ahead past the end: unused
       load_pair(p, X[kPhase >> 1], Y[kPhase >> 1]);
     }
     if constexpr (kPhase == 0) {
-      int64_t gi = (t >> 2) + 1;
+      int gi = (t >> 2) + 1;
       if (gi > ngroups - 1) gi = ngroups - 1;
       load_group(g, gi, nxt);
     }
@@ -437,11 +437,11 @@ struct DgradProducer : DgradStore, PerStepLoads<kDQ, DgradProducer<kDQ>> {
     am_idx = (int64_t)r * (g.wk >> 6) + (cc >> 6);
     am = g.am;
   }
-  __device__ __forceinline__ void load_step(const GemmArgs &g, int64_t step, u32x4 &w,
+  __device__ __forceinline__ void load_step(const GemmArgs &g, int step, u32x4 &w,
                                             AbsRaw &a) const {
     // Step s covers W rows 64s .. 64s+63.
-    w = *reinterpret_cast<const u32x4 *>(ptr + step * 64 * (g.wk >> 1));
-    a = absmax_load<kDQ>(am, am_idx + step * 64 * (g.wk >> 6));
+    w = *reinterpret_cast<const u32x4 *>(ptr + (int64_t)step * 64 * (g.wk >> 1));
+    a = absmax_load<kDQ>(am, am_idx + (int64_t)step * 64 * (g.wk >> 6));
   }
 };
 
@@ -464,7 +464,7 @@ struct DgradBatchProducer : DgradStore {
   int64_t pstride;          // packed bytes per step (64 W rows)
   int64_t gblk;             // absmax block (row r + 64q, blocks b0, b0 + 1) of group 0
   int64_t gstride;          // blocks per group of 4 steps (256 W rows)
-  int64_t ngroups;
+  int ngroups;
   uint32_t shift;           // 8 * (q >> 1): the thread's block within the pair
   AbsmaxRef am;
   u32x4 w[2];
@@ -478,12 +478,12 @@ struct DgradBatchProducer : DgradStore {
     pstride = 64 * (g.wk >> 1);
     gblk = (int64_t)(r + 64 * q) * (g.wk >> 6) + (o0 >> 6);
     gstride = 256 * (g.wk >> 6);
-    ngroups = g.R >> 8;
+    ngroups = (int)(g.R >> 8);
     shift = 8u * (uint32_t)(q >> 1);
     am = g.am;
   }
-  __device__ __forceinline__ void load_group(int64_t gi, u32x2 &v) const {
-    const int64_t blk = gblk + gi * gstride;
+  __device__ __forceinline__ void load_group(int gi, u32x2 &v) const {
+    const int64_t blk = gblk + (int64_t)gi * gstride;
     if constexpr (kDQ) {
       v.x = *reinterpret_cast<const uint16_t *>(am.q + blk);
       v.y = __builtin_bit_cast(uint32_t, am.scale[blk >> am.group_shift]);
@@ -504,10 +504,10 @@ struct DgradBatchProducer : DgradStore {
       return __builtin_bit_cast(float, shift != 0u ? by : bx);
     }
   }
-  __device__ __forceinline__ void load_words(int64_t step, u32x4 &v) const {
-    v = *reinterpret_cast<const u32x4 *>(ptr + step * pstride);
+  __device__ __forceinline__ void load_words(int step, u32x4 &v) const {
+    v = *reinterpret_cast<const u32x4 *>(ptr + (int64_t)step * pstride);
   }
-  __device__ __forceinline__ void prologue_load(const GemmArgs &g, int64_t nsteps) {
+  __device__ __forceinline__ void prologue_load(const GemmArgs &g, int nsteps) {
     (void)g;
     load_words(0, w0);
     load_words(nsteps > 1 ? 1 : 0, w[1]);
@@ -517,12 +517,12 @@ struct DgradBatchProducer : DgradStore {
     store_tile(lds, w0, masked(group_absmax<0>(cur)));
   }
   template <int kPhase>
-  __device__ __forceinline__ void issue_loads(const GemmArgs &g, int64_t t, int64_t nsteps) {
+  __device__ __forceinline__ void issue_loads(const GemmArgs &g, int t, int nsteps) {
     (void)g;
-    const int64_t t2 = (t + 2 < nsteps) ? t + 2 : nsteps - 1;
+    const int t2 = (t + 2 < nsteps) ? t + 2 : nsteps - 1;
     load_words(t2, w[kPhase & 1]);
     if constexpr (kPhase == 0) {
-      int64_t gi = (t >> 2) + 1;
+      int gi = (t >> 2) + 1;
       if (gi > ngroups - 1) gi = ngroups - 1;  // look-ahead past the end: unused
       load_group(gi, nxt);
     }
@@ -667,18 +667,18 @@ __device__ __forceinline__ void gemm_step(const GemmArgs &g, Producer &prod,
                                           u32x4 (&b)[2][4], u32x4 *Acur, u32x4 *Aoth,
                                           const u32x4 *Bcur, u32x4 *Bnext,
                                           __amdgpu_buffer_rsrc_t arsrc, const uint32_t (&aoff)[16],
-                                          int64_t t, int64_t nsteps, int jl, int grp) {
+                                          int t, int nsteps, int jl, int grp) {
   constexpr int kPar = 1 - (kPhase & 1);
   constexpr bool kFwd = Producer::kFwd;
   constexpr int kWordStages = 6;
-  const int64_t t1 = (t + 1 < nsteps) ? t + 1 : nsteps - 1;
-  const int64_t t2 = (t + 2 < nsteps) ? t + 2 : nsteps - 1;
+  const int t1 = (t + 1 < nsteps) ? t + 1 : nsteps - 1;
+  const int t2 = (t + 2 < nsteps) ? t + 2 : nsteps - 1;
   Lut16 lut;
   uint32_t lutd[2];
   NatLookup wl;
   uint32_t wp[4][4];  // dequantized elements of each packed word, memory order
   float ta = 0.0f;
-  auto dma = [&](u32x4 *dst, int d, int64_t step) {
+  auto dma = [&](u32x4 *dst, int d, int step) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(arsrc, (lds_void_t *)(dst + d * 64), 16,
                                              (int)aoff[d], (int)(step * (kStep * 2)), 0, 0);
   };
@@ -769,7 +769,7 @@ __device__ __forceinline__ void gemm_main(const GemmArgs &g, Producer &prod,
                                           floatx16 (&acc)[4][4], u32x4 *__restrict__ A0,
                                           u32x4 *__restrict__ A1, u32x4 *__restrict__ B0,
                                           u32x4 *__restrict__ B1, __amdgpu_buffer_rsrc_t arsrc,
-                                          const uint32_t (&aoff)[16], int64_t nsteps, int jl,
+                                          const uint32_t (&aoff)[16], int nsteps, int jl,
                                           int grp) {
   // Prologue: the producer's loads for steps 0 and 1, the activation tile of
   // step 0 and rows 0-63 of step 1 (DMA), then the weight tile of step 0
@@ -807,7 +807,7 @@ __device__ __forceinline__ void gemm_main(const GemmArgs &g, Producer &prod,
   // with kUnroll 4 needs nsteps % 4 == 0 (checked at launch); with kUnroll 2
   // an odd last step runs alone.
   constexpr int U = Producer::kUnroll;
-  int64_t t = 0;
+  int t = 0;
 #pragma unroll 1
   for (; t + U <= nsteps; t += U) {
     static_for<0, U>([&](auto P) {
@@ -1146,7 +1146,7 @@ __global__ void __launch_bounds__(kGemmThreads, 1) nf4_gemm_fwd_kernel(const Gro
     floatx16 acc[4][4];
     zero_acc(acc);
     gemm_main<Producer>(g, prod, acc, &g_lds_a[wave][0][0], &g_lds_a[wave][1][0], g_lds_b[0],
-                        g_lds_b[1], arsrc, aoff, g.R / kStep, jl, grp);
+                        g_lds_b[1], arsrc, aoff, (int)(g.R / kStep), jl, grp);
     if (slice < 0) {
       epilogue(g, acc, wave, m0, o0, lane);
     } else {
@@ -1332,7 +1332,7 @@ __global__ void __launch_bounds__(kGemmThreads, 1) nf4_gemm_swiglu_kernel(const 
     floatx16 acc[4][4];
     zero_acc(acc);
     gemm_main<Producer>(g, prod, acc, &g_lds_a[wave][0][0], &g_lds_a[wave][1][0], g_lds_b[0],
-                        g_lds_b[1], arsrc, aoff, g.R / kStep, jl, grp);
+                        g_lds_b[1], arsrc, aoff, (int)(g.R / kStep), jl, grp);
     store_swiglu(g, acc, m0, c0, jl, grp);
   }
 }
@@ -1370,7 +1370,7 @@ __global__ void __launch_bounds__(kGemmThreads, 1) nf4_gemm_dgrad_kernel(const G
       Producer prod;
       prod.init(g, o0, (uint32_t)(uintptr_t)(lds_void_t *)&g_lds_b[0][0]);
       gemm_main<Producer>(g, prod, acc, &g_lds_a[wave][0][0], &g_lds_a[wave][1][0], g_lds_b[0],
-                          g_lds_b[1], arsrc, aoff, g.R / kStep, jl, grp);
+                          g_lds_b[1], arsrc, aoff, (int)(g.R / kStep), jl, grp);
     }
     store_tile(g, acc, m0, o0, jl, grp);
   }
@@ -1407,7 +1407,8 @@ static int32_t check_gemm(const uint16_t *act, const nf4s_tensor *w, int64_t m, 
   return NF4S_OK;
 }
 
-// The activation loads address a wave's 128 rows with 32-bit offsets.
+// The activation loads address a wave's 128 rows with 32-bit offsets.  The
+// bound also keeps the kernels' 32-bit step counts (R / 64 <= 2^16) exact.
 static int32_t check_offsets(int64_t lda) {
   if (lda > (int64_t)1 << 22)
     return fail(NF4S_ERR_UNSUPPORTED_SHAPE, "activation row of %lld elements is too long",
