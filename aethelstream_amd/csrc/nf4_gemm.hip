@@ -906,51 +906,11 @@ __device__ __forceinline__ void zero_acc(floatx16 (&acc)[4][4]) {
 // their first operand, so each accumulator tile is the transposed output
 // block: lane l holds activation row m0 + 32mt + l%32 and output columns
 // o0 + 32nt + 8j + 4g + i (i = 0..3) in registers 4j + i.  Four adjacent
-// columns leave as one 8-byte store.
+// columns leave as one 8-byte store.  This is the path for outputs that do
+// not take 16-byte stores (store_tile_lds takes the others).
 __device__ __forceinline__ void store_tile(const GemmArgs &g, const floatx16 (&acc)[4][4],
                                            int64_t m0, int64_t o0, int jl, int grp) {
   const bool vec_ok = ((reinterpret_cast<uintptr_t>(g.out) & 7) == 0) && ((g.ldo & 3) == 0);
-  // Whole-width tile with 16-byte stores: lanes l and l + 32 pair their
-  // 8-byte halves with v_permlane32_swap (as store_tile_lds does), and each
-  // lane stores whole 16-byte chunks through a buffer resource that ends after
-  // the wave's last row below M: 32 branch-free stores, each instruction 32
-  // rows x 32 contiguous bytes, instead of 64 8-byte stores with a test per
-  // row.  Input gradient, same-box A/B: +1.4 to +1.7 % (70B q and down, 7B
-  // gate), 70B gate unchanged.
-  if (((reinterpret_cast<uintptr_t>(g.out) & 15) == 0) && ((g.ldo & 7) == 0) &&
-      o0 + kTileO <= g.O && g.ldo < ((int64_t)1 << 23)) {
-    const int64_t left = g.M - m0;
-    const int64_t rows = left <= 0 ? 0 : (left > 128 ? 128 : left);
-    const uint32_t ldo2 = (uint32_t)(g.ldo * 2);  // < 2^24: every offset fits 32 bits
-    const uint16_t *base = rows > 0 ? g.out + m0 * g.ldo + o0 : g.out;
-    const int32_t nrec = rows > 0 ? (int32_t)((rows - 1) * ldo2 + kTileO * 2) : 0;
-    const __amdgpu_buffer_rsrc_t rs =
-        __builtin_amdgcn_make_buffer_rsrc((void *)base, 0, nrec, kBufferFlags);
-    typedef unsigned int uvec4 __attribute__((ext_vector_type(4)));
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-      const uint32_t rowoff = (uint32_t)(32 * mt + jl) * ldo2;
-#pragma unroll
-      for (int nt = 0; nt < 4; ++nt) {
-        uint32_t lo[4], hi[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          lo[j] = pack_bf16x2(acc[mt][nt][4 * j], acc[mt][nt][4 * j + 1]);
-          hi[j] = pack_bf16x2(acc[mt][nt][4 * j + 2], acc[mt][nt][4 * j + 3]);
-        }
-#pragma unroll
-        for (int jp = 0; jp < 4; jp += 2) {
-          const auto a = __builtin_amdgcn_permlane32_swap(lo[jp], lo[jp + 1], false, false);
-          const auto b = __builtin_amdgcn_permlane32_swap(hi[jp], hi[jp + 1], false, false);
-          const uint32_t a0 = a[0], a1 = a[1], b0 = b[0], b1 = b[1];
-          const int c = 4 * nt + jp + grp;
-          __builtin_amdgcn_raw_buffer_store_b128((uvec4){a0, b0, a1, b1}, rs,
-                                                 (int)(rowoff + 16u * (uint32_t)c), 0, 0);
-        }
-      }
-    }
-    return;
-  }
   const int64_t cl = g.O - (o0 + 4 * grp);
   const int32_t clim = (int32_t)(cl < 0 ? 0 : (cl > (1 << 30) ? (1 << 30) : cl));
 #pragma unroll
@@ -1001,6 +961,11 @@ __device__ __forceinline__ void store_tile(const GemmArgs &g, const floatx16 (&a
 //     columns keeps the row-by-row stores.
 __device__ __forceinline__ void store_tile_lds(const GemmArgs &g, const floatx16 (&acc)[4][4],
                                                u32x4 *lds, int64_t m0, int64_t o0, int lane) {
+  // The lane's 32 + 32 LDS addresses below depend on nothing that changes
+  // between tiles; an opaque copy of the lane index keeps the compiler from
+  // hoisting them out of the tile loop, where they are spilled and reloaded
+  // here, each reload waiting for every outstanding memory access.
+  asm volatile("" : "+v"(lane));
   const int jl = lane & 31, grp = lane >> 5;
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt) {
@@ -1074,9 +1039,13 @@ __device__ __forceinline__ void store_tile_lds(const GemmArgs &g, const floatx16
   }
 }
 
-// The forward kernel's epilogue: through LDS when 16-byte stores fit.  (The
-// input-gradient kernel stores straight from the accumulators: its tiles
-// measured no faster through LDS.)
+// The forward and input-gradient epilogue: through LDS when 16-byte stores
+// fit.  For the input gradient, against its direct lane-paired stores
+// (store_tile), same-box A/B, two rounds: 70B q +0.9-1.1 %, 70B down
+// +1.5-3.5 %, 7B gate +1.5-4 %, summed gate/up +0.2-0.5 %.  (An earlier
+// try measured -1 %: the compiler then hoisted the read-back addresses out
+// of the tile loop and spilled 57 registers; store_tile_lds now keeps them
+// in place.)
 __device__ __forceinline__ void epilogue(const GemmArgs &g, const floatx16 (&acc)[4][4], int wave,
                                          int64_t m0, int64_t o0, int lane) {
   if (((reinterpret_cast<uintptr_t>(g.out) & 15) == 0) && ((g.ldo & 7) == 0))
@@ -1372,7 +1341,7 @@ __global__ void __launch_bounds__(kGemmThreads, 1) nf4_gemm_dgrad_kernel(const G
       gemm_main<Producer>(g, prod, acc, &g_lds_a[wave][0][0], &g_lds_a[wave][1][0], g_lds_b[0],
                           g_lds_b[1], arsrc, aoff, (int)(g.R / kStep), jl, grp);
     }
-    store_tile(g, acc, m0, o0, jl, grp);
+    epilogue(g, acc, wave, m0, o0, lane);
   }
 }
 

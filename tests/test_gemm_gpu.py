@@ -446,6 +446,35 @@ def test_random_shapes_fwd_and_dgrad(case):
     assert rel_l2(dx.float().cpu().numpy(), ref.cpu().numpy()) <= TOL_SAME
 
 
+# Both epilogues: outputs that take 16-byte stores go through the LDS
+# read-back (store_tile_lds), the others through direct 8-byte or element
+# stores (store_tile).  The same accumulators must give the same bits either
+# way: outputs whose base is 2 bytes off 16-byte alignment take the direct
+# path.  Ragged rows and a ragged last output tile on both kernels.
+@pytest.mark.parametrize("m,n,k,dq", [(300, 256, 256, True), (777, 640, 384, False),
+                                      (1024, 136, 512, True)])
+def test_unaligned_output_equals_aligned(m, n, k, dq):
+    print(f"epilogue paths m={m} n={n} k={k} dq={dq}", flush=True)
+    x, _ = _act(m, k, 700 + m)
+    w = _weight(n, k, 710 + n, dq)
+    y = gemm.linear_fwd(x, w, split_k=False)
+    flat = torch.empty(m * n + 8, dtype=torch.bfloat16, device=DEV)
+    y_off = flat[1:1 + m * n].view(m, n)
+    gemm.linear_fwd(x, w, out=y_off, split_k=False)
+    dy, _ = _act(m, n - n % 64 if n % 64 else n, 720 + m)
+    wd = _weight(dy.shape[1], k, 730 + n, dq)
+    dx = gemm.linear_dgrad(dy, wd)
+    flat2 = torch.empty(m * k + 8, dtype=torch.bfloat16, device=DEV)
+    dx_off = flat2[1:1 + m * k].view(m, k)
+    gemm.linear_dgrad(dy, wd, out=dx_off)
+    torch.cuda.synchronize()
+    assert y_off.data_ptr() % 16 == 2 and dx_off.data_ptr() % 16 == 2
+    assert torch.equal(y.view(torch.int16), y_off.view(torch.int16))
+    assert torch.equal(dx.view(torch.int16), dx_off.view(torch.int16))
+    ref = x.float() @ nf4.dequant(w).float().t()
+    assert rel_l2(y.float().cpu().numpy(), ref.cpu().numpy()) <= TOL_SAME
+
+
 # 64 output tiles per 512-row block switch the tile order to XCD pairs
 # sharing a row block (tiles_m % 4 == 0): ragged rows and a ragged last
 # output tile under that order, forward (n) and input gradient (k).
