@@ -31,7 +31,30 @@ struct WgradArgs {
   int64_t M, N, K;
   int32_t tiles_n, tiles_k;
   int32_t accumulate;
+  int32_t blk_n, blk_k;  // XCD block of blk_n x blk_k tiles (0: map_tile order)
 };
+
+// Tile order of a launch whose rounds are all full (T a multiple of the
+// grid G, G / 8 slots per XCD): in round r, XCD x (workgroups b with
+// b % 8 == x) takes block 8 r + x of blk_n x blk_k tiles, blk_n * blk_k =
+// G / 8, slot i = (b % G) / 8 the tile (i / blk_k, i % blk_k) of the block.
+// The XCD's workgroups then read blk_n dy column blocks and blk_k x column
+// blocks per 64-token step (4 + 8 = 12 x 32 KB on a 256-CU part) instead of
+// 1 + 32 in map_tile's order, where they share one dy block and read every
+// x block of the row; the rest comes from the XCD's L2.
+__device__ __forceinline__ void wg_map_tile(const WgradArgs &g, int b, int &tn, int &tk) {
+  if (g.blk_n == 0) {
+    map_tile(b, g.tiles_n, g.tiles_k, tn, tk);
+    return;
+  }
+  const int G = gridDim.x;
+  const int r = b / G, c = b - r * G;
+  const int blk = 8 * r + (c & 7), i = c >> 3;
+  const int nbk = g.tiles_k / g.blk_k;
+  const int bn = blk / nbk, bk = blk - bn * nbk;
+  tn = bn * g.blk_n + i / g.blk_k;
+  tk = bk * g.blk_k + i % g.blk_k;
+}
 
 // LDS tile: 64 token rows x 256 columns (512 B = 32 units of 16 B per row).
 // A wave reads one 128-column half (16 units).  Unit u of row r lives at
@@ -172,7 +195,7 @@ __global__ void __launch_bounds__(kWgThreads, 1) wgrad_kernel(const WgradArgs g)
 #pragma unroll 1
   for (int b = blockIdx.x; b < T; b += gridDim.x) {
     int tn, tk;
-    map_tile(b, g.tiles_n, g.tiles_k, tn, tk);
+    wg_map_tile(g, b, tn, tk);
     const int64_t n0 = (int64_t)tn * kWgTile, k0 = (int64_t)tk * kWgTile;
     // Buffer resources based at the tiles' first columns; num_records ends
     // at the matrix end, so token rows >= M (and the last row's columns past
@@ -313,6 +336,23 @@ static int32_t wgrad(const uint16_t *dy, const uint16_t *x, int64_t m, int64_t n
   g.accumulate = accumulate ? 1 : 0;
   const int64_t T = (int64_t)g.tiles_n * g.tiles_k;
   if (T > 0x7fffffff) return fail(NF4S_ERR_UNSUPPORTED_SHAPE, "too many tiles");
+  // XCD blocks (wg_map_tile) when every round is full: the squarest
+  // blk_n x blk_k = G / 8 that divides the tile grid.
+  const int64_t G = persistent_grid(T);
+  if (G % 8 == 0 && T % G == 0) {
+    const int S = (int)(G / 8);
+    int best = 0;
+    for (int bn = 1; bn <= S; ++bn) {
+      if (S % bn != 0 || g.tiles_n % bn != 0 || g.tiles_k % (S / bn) != 0) continue;
+      const int bk = S / bn;
+      const int cost = bn + bk;  // column blocks read per XCD and step
+      if (best == 0 || cost < best) {
+        best = cost;
+        g.blk_n = bn;
+        g.blk_k = bk;
+      }
+    }
+  }
   if (m == 0) {
     // An empty sum: dw += 0, or dw = 0 (a fill kernel rather than
     // hipMemsetAsync, so that a caller may capture the call in a HIP graph).
@@ -324,7 +364,7 @@ static int32_t wgrad(const uint16_t *dy, const uint16_t *x, int64_t m, int64_t n
                        0, s, dw, cnt);
     return check_launch("fill_zero_f32");
   }
-  hipLaunchKernelGGL(wgrad_kernel, dim3(persistent_grid(T)), dim3(kWgThreads), 0, s, g);
+  hipLaunchKernelGGL(wgrad_kernel, dim3((uint32_t)G), dim3(kWgThreads), 0, s, g);
   return check_launch("wgrad_kernel");
 }
 

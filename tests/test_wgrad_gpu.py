@@ -63,6 +63,26 @@ def test_wgrad_exact_on_integers():
     assert np.array_equal(dw.cpu().numpy(), ref)
 
 
+# Launches whose rounds are all full take the XCD-block tile order (each
+# XCD's workgroups cover 4 x 8 tiles per round): 256 and 512 tiles, with
+# ragged tokens, a ragged last tile row and accumulate.  Small integers make
+# every element exact, so this pins the order's tile coordinates bit for bit.
+@pytest.mark.parametrize("m,n,k,acc", [(64, 4096, 4096, False), (100, 8128, 2048, True),
+                                       (192, 2048, 16384, False)])
+def test_wgrad_xcd_block_order_exact(m, n, k, acc):
+    print(f"wgrad xcd blocks m={m} n={n} k={k} acc={acc}", flush=True)
+    g = torch.Generator().manual_seed(m + n)
+    dyi = torch.randint(-3, 4, (m, n), generator=g).float()
+    xi = torch.randint(-3, 4, (m, k), generator=g).float()
+    ref = dyi.double().t() @ xi.double()
+    dw = torch.full((n, k), 2.0 if acc else float("nan"), device=DEV)
+    gemm.linear_wgrad(dyi.to(DEV).to(torch.bfloat16), xi.to(DEV).to(torch.bfloat16), out=dw,
+                      accumulate=acc)
+    torch.cuda.synchronize()
+    want = (ref + 2.0 if acc else ref).float()
+    assert torch.equal(dw.cpu(), want)
+
+
 def test_wgrad_accumulate_two_micro_batches():
     """dW = sum over micro-batches (backward.rs:478-502): the second call
     accumulates into the first call's fp32 result; a smaller second batch."""
