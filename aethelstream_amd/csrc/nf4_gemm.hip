@@ -343,8 +343,8 @@ struct FwdBatchProducer : FwdStore {
 // columns o0..o0+127 (the output).  Thread -> (W row r = tid/4, quarter
 // q = tid%4): 32 consecutive columns of one block, dequantized as 4 words of
 // 8 elements and written as 4 16-B units.  The LDS tile keeps W's layout:
-// row r (256 B) holds the tile's 128 columns, unit u (columns 8u..8u+7) at
-// physical unit u ^ 5(r % 4).
+// row r (256 B) holds the tile's 128 columns; logical unit u (columns
+// 8u..8u+7) sits at physical unit (u ^ 2 (u / 8)) ^ 5 (r % 4).
 //
 // The MFMA fragment of output column o holds 8 consecutive reduction values,
 // a column of this tile.  ds_read_b64_tr_b16 transposes 4 x 4 blocks of
@@ -354,11 +354,15 @@ struct FwdBatchProducer : FwdStore {
 // lane i receives column i of rows 0..3, and two such reads (rows 0-3, 4-7)
 // make the fragment.
 //
-// Banks (64 x 4 B): a 16-lane group of the ds_write_b128 covers rows with
-// c = r % 4 = 0..3 at quarters 0..3 and one word k, physical units
-// 4(q ^ c) + (k ^ c), 16 distinct; a 32-lane half of a transposed read
-// covers c = 0..3 at units 4j..4j+3 (fragment j), physical units
-// 4(j ^ c) + (u % 4 ^ c), 16 distinct.
+// Banks: a ds_write_b128 is served 8 lanes at a time over a 128-B window
+// (bank group = address / 16 mod 8; measured with an LDS probe: the plain
+// XOR layout u ^ 5 (r % 4) cost 8 conflict cycles per store, this one none).
+// Its 8 lanes are rows r, r + 1 (c = r % 4 and c + 1) at quarters 0..3 and
+// one word k: physical units 4 (q ^ c) + ((k ^ 2 (q / 2)) ^ c), whose values
+// mod 8 are {k', 4 + k', k' ^ 2, 4 + (k' ^ 2)} for k' = k ^ c, disjoint for
+// the two rows.  A 32-lane half of a transposed read covers c = 0..3 at
+// logical units 4j..4j+3 (fragment j), physical units
+// 4 (j ^ c) + ((u % 4 ^ 2 (j / 2)) ^ c), 16 distinct.
 // DgradStore holds the thread mapping, the LDS stores and the transposed
 // fragment reads; the two input-gradient producers differ only in how the
 // packed words and absmax reach the registers.
@@ -370,13 +374,13 @@ struct DgradStore {
   __device__ void init_layout(const GemmArgs &g, int64_t o0) {
     const int r = threadIdx.x >> 2, q = threadIdx.x & 3, c = r & 3;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) sidx[k] = 16 * r + 4 * (q ^ c) + (k ^ c);
+    for (int k = 0; k < 4; ++k) sidx[k] = 16 * r + 4 * (q ^ c) + ((k ^ (2 * (q >> 1))) ^ c);
     const int lane = threadIdx.x & 63, l16 = lane & 15, cr = l16 >> 2;
     const int ub = 2 * ((lane >> 4) & 1) + ((l16 >> 1) & 1);  // unit within the fragment's 4
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      roff[j] = (uint32_t)(256 * (8 * (lane >> 5) + cr) + 16 * (4 * (j ^ cr) + (ub ^ cr)) +
-                           8 * (l16 & 1));
+      roff[j] = (uint32_t)(256 * (8 * (lane >> 5) + cr) +
+                           16 * (4 * (j ^ cr) + ((ub ^ (2 * (j >> 1))) ^ cr)) + 8 * (l16 & 1));
     valid_mask = (o0 + 32 * q < g.wk) ? 0xffffffffu : 0u;
   }
   // Columns beyond k read column 0's bytes and are zeroed via the absmax.
