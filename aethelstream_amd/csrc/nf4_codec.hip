@@ -63,37 +63,176 @@ __device__ __forceinline__ float load_elem<uint16_t>(const uint16_t *x, int64_t 
   return __builtin_bit_cast(float, (uint32_t)x[e] << 16);
 }
 
-// One 64-element block by one wave, one lane per element: returns the block's
-// unclamped absmax (in every lane) and writes its packed codes.
-template <typename T>
-__device__ __forceinline__ float quantize_block64(const T *__restrict__ x, int64_t n, int64_t b,
-                                                  int lane, uint8_t *__restrict__ packed) {
-  const int64_t e = b * 64 + lane;
-  const float v = (e < n) ? load_elem<T>(x, e) : 0.0f;  // zero padding, quantizer.py:30-32
-  float m = fabsf(v);
+// ---- Block-64 quantize: 8 elements per lane, 8 lanes per block ----------
+//
+// The code rule above is monotone in n (within a bracket the rounded
+// distance to the lower code only grows and to the upper one only shrinks),
+// so it is a step function of the fp32 quotient: code(n) = #{k : n >= S_k}
+// for the 15 fp32 thresholds below (the smallest fp32 n with code(n) >= k;
+// nf4_code_steps.py derives them from the codebook, and an exhaustive CPU
+// check over every fp32 in [-1, 1] compares the step form with the 16-way
+// argmin).
+__constant__ uint32_t kStepBits[15] = {
+    0xbf591cd8u, 0xbf1c5270u, 0xbeeb847fu, 0xbeadea76u, 0xbe703cecu,
+    0xbe0d38bbu, 0xbd3a7871u, 0x3d22fb00u, 0x3df64863u, 0x3e5067e1u,
+    0x3e9582d5u, 0x3ec753fau, 0x3f006d04u, 0x3f248db0u, 0x3f5c89dau,
+};
+
+// Lookup: bucket i = floor(16 q + 16) covers q in [-1 + i/16, -1 + (i+1)/16);
+// consecutive steps are >= 0.08 apart, so a bucket holds at most one, and
+// every step is >= 0.0016 from every bucket edge, so an index that rounding
+// puts in the neighbouring bucket still counts the same steps.  Entry i =
+// {that step's bits (+inf if none), number of steps below the bucket}; the
+// code is base + (q >= step).  Bucket 32 (q = 1) has base 15.
+constexpr int kBuckets = 33;
+
+__device__ __forceinline__ void init_step_table(uint2 *tab) {
+  const int i = (int)threadIdx.x;
+  if (i < kBuckets) {
+    const float lo = -1.0f + 0.0625f * (float)i, hi = lo + 0.0625f;
+    uint32_t base = 0, step = 0x7f800000u;
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) m = max_nan(m, __shfl_xor(m, off, 64));
-  const float safe = (m < 1e-8f) ? 1e-8f : m;          // clamp(min=1e-8), :36
-  const float nv = v / safe;                           // correctly rounded, :38
-  uint32_t c = nf4_code(nv);
-  uint32_t c1 = __shfl_xor(c, 1, 64);
-  if (e + 1 >= n) c1 = 0;                              // odd-count pad nibble, :44-45
-  if ((lane & 1) == 0 && e < n) packed[e >> 1] = (uint8_t)((c << 4) | c1);  // :46
-  return m;                                            // unclamped, :48-53
+    for (int k = 0; k < 15; ++k) {
+      const float t = __builtin_bit_cast(float, kStepBits[k]);
+      base += (t < lo) ? 1u : 0u;
+      if (t >= lo && t < hi) step = kStepBits[k];
+    }
+    tab[i] = make_uint2(step, base);
+  }
 }
 
-// block_size == 64: one wave per block.
-template <typename T>
+// Fast quotients q' = v * RN(1/s) are within 1.5 ulp + 2^-24 |q| < 2^-23 of
+// v / s, and the exact RN(v / s) within 2^-25 of it, so q' and RN(v / s) can
+// only fall on different sides of a step lying within 2^-22 of q'.  Every
+// q' within kMargin of its bucket's step marks the lane for the exact
+// quotient (the bucket's step is the only one within 0.0016 of q').
+constexpr float kMargin = 0x1p-20f;
+
+__device__ __forceinline__ uint32_t step_code(const uint2 *tab, float q, bool &near) {
+  q = fmaxf(q, -1.0f);  // NaN -> -1 -> code 0 (argmin over NaN distances is 0)
+  const uint32_t i = (uint32_t)__builtin_fmaf(q, 16.0f, 16.0f);  // |q| <= 1 + 2^-23: i <= 32
+  const uint2 t = tab[i];
+  const float step = __builtin_bit_cast(float, t.x);
+  near |= fabsf(q - step) <= kMargin;
+  return t.y + ((q >= step) ? 1u : 0u);
+}
+
+// The lane's 8 elements e0 .. e0+7, zero past `lim` (quantizer.py:30-32).
+template <typename T, bool kVec>
+__device__ __forceinline__ void load8(const T *__restrict__ x, int64_t lim, int64_t e0,
+                                      float v[8]) {
+  if (kVec && e0 + 8 <= lim) {
+    if constexpr (sizeof(T) == 4) {
+      // Elements go through scalar temporaries: hipcc folds a bit_cast of a
+      // vector-element subscript to element 0 for every index.
+      const u32x4 a = *(const u32x4 *)(x + e0);
+      const u32x4 b = *(const u32x4 *)(x + e0 + 4);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const uint32_t ak = a[k], bk = b[k];
+        v[k] = __builtin_bit_cast(float, ak);
+        v[4 + k] = __builtin_bit_cast(float, bk);
+      }
+    } else {
+      const u32x4 a = *(const u32x4 *)(x + e0);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const uint32_t ak = a[k];
+        v[2 * k] = __builtin_bit_cast(float, ak << 16);
+        v[2 * k + 1] = __builtin_bit_cast(float, ak & 0xffff0000u);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = (e0 + k < lim) ? load_elem<T>(x, e0 + k) : 0.0f;
+  }
+}
+
+// max(m, m of the lane that DPP control kCtrl names), NaN-propagating.
+template <int kCtrl>
+__device__ __forceinline__ float dpp_max(float m) {
+  const int o = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, m), kCtrl, 0xF, 0xF, false);
+  return __builtin_elementwise_maximum(m, __builtin_bit_cast(float, o));
+}
+
+// Codes of the lane's 8 elements, packed as quantizer.py:43-46 packs them
+// (even element in the high nibble), and the block's unclamped absmax
+// (:35, :48-53) in every lane of the block.  Call with the whole wave
+// active: the absmax is reduced across the block's 8 lanes with DPP moves
+// (quad xor 1, quad xor 2, half-row mirror).
+__device__ __forceinline__ float encode8(const uint2 *tab, const float v[8], int64_t e0,
+                                         int64_t lim, uint32_t &word) {
+  float m = __builtin_elementwise_maximum(fabsf(v[0]), fabsf(v[1]));  // NaN-propagating, :35
+#pragma unroll
+  for (int k = 2; k < 8; ++k) m = __builtin_elementwise_maximum(m, fabsf(v[k]));
+  m = dpp_max<0xB1>(m);   // quad_perm [1,0,3,2]
+  m = dpp_max<0x4E>(m);   // quad_perm [2,3,0,1]
+  m = dpp_max<0x141>(m);  // row_half_mirror: lane i <-> 7-i within 8
+  const float s = (m < 1e-8f) ? 1e-8f : m;  // clamp(min=1e-8), :36 (NaN stays NaN)
+  const float y = 1.0f / s;                 // correctly rounded
+  uint32_t c[8];
+  bool near = false;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) c[k] = step_code(tab, v[k] * y, near);
+  if (near) {  // rare: redo the lane with the correctly rounded quotient, :38
+    bool unused = false;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) c[k] = step_code(tab, v[k] / s, unused);
+  }
+  if (e0 + 8 > lim) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      if (e0 + k >= lim) c[k] = 0;  // odd-count pad nibble, :44-45
+  }
+  word = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) word |= ((c[2 * j] << 4) | c[2 * j + 1]) << (8 * j);
+  return m;
+}
+
+// Bytes e0/2 .. e0/2+3 of the packed output, those below ceil(lim/2).
+template <bool kVec>
+__device__ __forceinline__ void store_codes(uint8_t *__restrict__ packed, int64_t e0,
+                                            int64_t lim, uint32_t word) {
+  if (kVec && e0 + 8 <= lim) {
+    *(uint32_t *)(packed + (e0 >> 1)) = word;
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (e0 + 2 * j < lim) packed[(e0 >> 1) + j] = (uint8_t)(word >> (8 * j));
+  }
+}
+
+// A tile is 8 blocks (512 elements) by one wave; lane l holds elements
+// 8l .. 8l+7, so the wave reads 2 KB and writes 256 B contiguously.  Each
+// wave takes kU consecutive tiles per pass (loads of all kU issued first).
+// kVec: x 16-byte and packed 4-byte aligned (16-byte loads, 4-byte stores).
+template <typename T, bool kVec, int kU>
 __global__ void __launch_bounds__(256) quantize64_kernel(const T *__restrict__ x, int64_t n,
                                                          uint8_t *__restrict__ packed,
                                                          float *__restrict__ absmax,
-                                                         int64_t nblocks) {
+                                                         int64_t ntiles) {
+  __shared__ uint2 tab[kBuckets];
+  init_step_table(tab);
+  __syncthreads();
   const int lane = threadIdx.x & 63;
-  const int64_t wave0 = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-  const int64_t nwaves = (int64_t)gridDim.x * (blockDim.x >> 6);
-  for (int64_t b = wave0; b < nblocks; b += nwaves) {
-    const float m = quantize_block64<T>(x, n, b, lane, packed);
-    if (lane == 0) absmax[b] = m;
+  const int64_t nwaves = (int64_t)gridDim.x * 4;
+  for (int64_t w = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); w * kU < ntiles; w += nwaves) {
+    float v[kU][8];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) load8<T, kVec>(x, n, (w * kU + u) * 512 + 8 * lane, v[u]);
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int64_t t = w * kU + u;
+      if (t >= ntiles) break;  // wave-uniform
+      const int64_t e0 = t * 512 + 8 * lane;
+      uint32_t word;
+      const float m = encode8(tab, v[u], e0, n, word);
+      if (e0 < n) {
+        store_codes<kVec>(packed, e0, n, word);
+        if ((lane & 7) == 0) absmax[t * 8 + (lane >> 3)] = m;  // :48-53, unclamped
+      }
+    }
   }
 }
 
@@ -175,11 +314,12 @@ __global__ void __launch_bounds__(256) dq_encode_kernel(const float *__restrict_
 // Quantize + double-quant in one pass, for weights re-quantized on the device
 // after an update (FlowCast::on_weights_updated, flowcast/src/lib.rs:501-521,
 // after apply_galore_bf16_update, doublepass/src/precision.rs:187-202): one
-// workgroup per group of `group` 64-element blocks.
+// workgroup per group of `group` 64-element blocks, its waves taking the
+// group's 8-block tiles in turn (the same lane code as quantize64_kernel).
 // The block absmax stay in LDS (never written as fp32), so the call needs no
 // scratch memory; codes come from the fp32 absmax exactly as quantize64_kernel
 // computes them, and q / scale exactly as dq_encode_kernel does.
-template <typename T>
+template <typename T, bool kVec, int kU>
 __global__ void __launch_bounds__(256) quantize_dq_kernel(const T *__restrict__ x, int64_t n,
                                                           int32_t group,
                                                           uint8_t *__restrict__ packed,
@@ -187,13 +327,34 @@ __global__ void __launch_bounds__(256) quantize_dq_kernel(const T *__restrict__ 
                                                           float *__restrict__ scale,
                                                           int64_t nblocks) {
   extern __shared__ float am_lds[];  // `group` block absmax
+  __shared__ uint2 tab[kBuckets];
   __shared__ float red[4];
+  init_step_table(tab);
+  __syncthreads();
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t b0 = (int64_t)blockIdx.x * group;
   const int64_t nb = (b0 + group < nblocks) ? group : nblocks - b0;
-  for (int64_t i = wave; i < nb; i += 4) {
-    const float m = quantize_block64<T>(x, n, b0 + i, lane, packed);
-    if (lane == 0) am_lds[i] = m;
+  // Elements of this group's blocks: the others read as absent, so a tile
+  // that runs past the group (group < 8) neither counts nor writes them.
+  const int64_t lim = (64 * (b0 + nb) < n) ? 64 * (b0 + nb) : n;
+  const int ntl = (int)((nb + 7) >> 3);
+  for (int w = wave; w * kU < ntl; w += 4) {
+    float v[kU][8];
+#pragma unroll
+    for (int u = 0; u < kU; ++u)
+      load8<T, kVec>(x, lim, (b0 + 8 * (w * kU + u)) * 64 + 8 * lane, v[u]);
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int t = w * kU + u;
+      if (t >= ntl) break;  // wave-uniform
+      const int64_t e0 = (b0 + 8 * t) * 64 + 8 * lane;
+      uint32_t word;
+      const float m = encode8(tab, v[u], e0, lim, word);
+      if (e0 < lim) {
+        store_codes<kVec>(packed, e0, lim, word);
+        if ((lane & 7) == 0) am_lds[8 * t + (lane >> 3)] = m;
+      }
+    }
   }
   __syncthreads();
   float m = 0.0f;
@@ -389,6 +550,26 @@ static int32_t dequant_batch(const nf4s_tensor *ts, const int64_t *ns, uint16_t 
   return NF4S_OK;
 }
 
+constexpr int kQuantU = 2;  // tiles per wave pass
+
+template <typename T>
+static bool quantize_vec_ok(const T *x, const uint8_t *packed) {
+  return ((uintptr_t)x % 16 == 0) && ((uintptr_t)packed % 4 == 0);
+}
+
+template <typename T>
+static int32_t quantize64(const T *x, int64_t n, uint8_t *packed, float *absmax, hipStream_t s) {
+  const int64_t ntiles = (n + 511) / 512;
+  const int grid = grid_for((ntiles + kQuantU - 1) / kQuantU, 4);
+  if (quantize_vec_ok(x, packed))
+    hipLaunchKernelGGL((quantize64_kernel<T, true, kQuantU>), dim3(grid), dim3(256), 0, s, x, n,
+                       packed, absmax, ntiles);
+  else
+    hipLaunchKernelGGL((quantize64_kernel<T, false, kQuantU>), dim3(grid), dim3(256), 0, s, x, n,
+                       packed, absmax, ntiles);
+  return check_launch("quantize64_kernel");
+}
+
 template <typename T>
 static int32_t quantize_dq(const T *x, int64_t n, int32_t block_size, int32_t group,
                            uint8_t *packed, uint8_t *q, float *scale, void *stream) {
@@ -405,9 +586,13 @@ static int32_t quantize_dq(const T *x, int64_t n, int32_t block_size, int32_t gr
   const int64_t nb = (n + 63) / 64;
   const int64_t ng = (nb + group - 1) / group;
   if (ng > 0x7fffffff) return fail(NF4S_ERR_UNSUPPORTED_SHAPE, "too many groups");
-  hipLaunchKernelGGL(quantize_dq_kernel<T>, dim3((uint32_t)ng), dim3(256),
-                     (size_t)group * sizeof(float), as_stream(stream), x, n, group, packed, q,
-                     scale, nb);
+  const size_t lds = (size_t)group * sizeof(float);
+  if (quantize_vec_ok(x, packed))
+    hipLaunchKernelGGL((quantize_dq_kernel<T, true, kQuantU>), dim3((uint32_t)ng), dim3(256), lds,
+                       as_stream(stream), x, n, group, packed, q, scale, nb);
+  else
+    hipLaunchKernelGGL((quantize_dq_kernel<T, false, kQuantU>), dim3((uint32_t)ng), dim3(256),
+                       lds, as_stream(stream), x, n, group, packed, q, scale, nb);
   return check_launch("quantize_dq_kernel");
 }
 
@@ -427,12 +612,7 @@ int32_t nf4s_quantize(const float *x, int64_t n, int32_t block_size, uint8_t *pa
     return fail(NF4S_ERR_INVALID_ARGUMENT, "NULL buffer");
   const int64_t nb = (n + block_size - 1) / block_size;
   hipStream_t s = as_stream(stream);
-  if (block_size == 64) {
-    const int64_t wg = (nb + 3) / 4;
-    hipLaunchKernelGGL(quantize64_kernel<float>, dim3(grid_for(wg, 1)), dim3(256), 0, s, x, n,
-                       packed, absmax, nb);
-    return check_launch("quantize64_kernel");
-  }
+  if (block_size == 64) return quantize64<float>(x, n, packed, absmax, s);
   hipLaunchKernelGGL(absmax_generic_kernel, dim3(grid_for(nb, 256)), dim3(256), 0, s, x, n,
                      block_size, absmax, nb);
   int32_t rc = check_launch("absmax_generic_kernel");
@@ -453,10 +633,7 @@ int32_t nf4s_quantize_bf16(const uint16_t *x, int64_t n, int32_t block_size, uin
   if (n == 0) return NF4S_OK;
   if (x == nullptr || packed == nullptr || absmax == nullptr)
     return fail(NF4S_ERR_INVALID_ARGUMENT, "NULL buffer");
-  const int64_t nb = (n + 63) / 64;
-  hipLaunchKernelGGL(quantize64_kernel<uint16_t>, dim3(grid_for((nb + 3) / 4, 1)), dim3(256), 0,
-                     as_stream(stream), x, n, packed, absmax, nb);
-  return check_launch("quantize64_kernel");
+  return quantize64<uint16_t>(x, n, packed, absmax, as_stream(stream));
 }
 
 int32_t nf4s_quantize_dq(const float *x, int64_t n, int32_t block_size, int32_t group,

@@ -47,6 +47,8 @@ def lib():
         L.or_nf4_code_bracket.restype = ctypes.c_uint8
         L.or_check_bracket_exhaustive.argtypes = [ctypes.c_int]
         L.or_check_bracket_exhaustive.restype = i64
+        L.or_check_steps_exhaustive.argtypes = [P, ctypes.c_int]
+        L.or_check_steps_exhaustive.restype = i64
         L.or_quantize_nf4.argtypes = [P, i64, i32, P, P]
         L.or_dq_encode.argtypes = [P, i64, i32, P, P]
         L.or_dq_decode.argtypes = [P, P, i64, i32, P]

@@ -128,6 +128,33 @@ int64_t or_check_bracket_exhaustive(int nthreads) {
     return bad;
 }
 
+/* A candidate step form of the same rule: code(n) = #{k : n >= steps[k]}
+ * for 15 ascending fp32 thresholds.  Returns how many fp32 n in [-1, 1]
+ * (every bit pattern, both signs) get a different code from the 16-way
+ * argmin of quantizer.py:40-41; 0 means the thresholds reproduce it. */
+int64_t or_check_steps_exhaustive(const float *steps, int nthreads) {
+    const uint32_t one = 0x3f800000u;
+    int64_t bad = 0;
+#ifdef _OPENMP
+    if (nthreads > 0) omp_set_num_threads(nthreads);
+#else
+    (void)nthreads;
+#endif
+#pragma omp parallel for reduction(+ : bad) schedule(static, 1 << 16)
+    for (int64_t b = 0; b <= (int64_t)one; ++b) {
+        const float p = u2f((uint32_t)b);
+        const float q = u2f((uint32_t)b | 0x80000000u);
+        int cp = 0, cq = 0;
+        for (int k = 0; k < 15; ++k) {
+            cp += p >= steps[k];
+            cq += q >= steps[k];
+        }
+        bad += or_nf4_code_argmin(p) != cp;
+        bad += or_nf4_code_argmin(q) != cq;
+    }
+    return bad;
+}
+
 /* quantizer.py:21-53. */
 void or_quantize_nf4(const float *x, int64_t n, int32_t bs, uint8_t *packed,
                      float *absmax) {

@@ -58,6 +58,7 @@ uint8_t or_nf4_code_bracket(float n);
  * every fp32 in [lo_bits..] of [-1, 1]; returns the number of mismatches.
  * nthreads <= 0 picks the OpenMP default. */
 int64_t or_check_bracket_exhaustive(int nthreads);
+int64_t or_check_steps_exhaustive(const float *steps, int nthreads);
 
 /* quantize_nf4 (shard_engine/python/pipeline/quantizer.py:21-53).
  * x: n fp32 values.  packed: ceil(n/2) bytes.  absmax: ceil(n/bs) floats

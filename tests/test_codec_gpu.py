@@ -278,3 +278,121 @@ def test_dq_planted_ties_round_half_even_on_device():
     np.testing.assert_array_equal(w.absmax_q.cpu().numpy(), q_ref)
     np.testing.assert_array_equal(w.absmax_scale.cpu().numpy().view(np.uint32),
                                   s_ref.view(np.uint32))
+
+
+# ---- Block-64 quantize: the step lookup and its exact-quotient fallback ----
+
+STEP_BITS = [0xbf591cd8, 0xbf1c5270, 0xbeeb847f, 0xbeadea76, 0xbe703cec, 0xbe0d38bb,
+             0xbd3a7871, 0x3d22fb00, 0x3df64863, 0x3e5067e1, 0x3e9582d5, 0x3ec753fa,
+             0x3f006d04, 0x3f248db0, 0x3f5c89da]
+# Block absmax (element 0 of each block) and the divisor it gives: the last
+# pair is below the 1e-8 clamp (quantizer.py:36).
+SCALES = [(1.0, 1.0), (0.0217, 0.0217), (1.5e-3, 1.5e-3), (7.77e4, 7.77e4),
+          (3.1e-37, 3.1e-37), (0.7071067, 0.7071067), (9e-9, 1e-8)]
+ULPS = [0, 1, 2, 3, 4, 6, 8, 12, 16, 24, 32, 64, 128, 256, 512, 1024, 4096, 16384]
+
+
+def _near(step_bits, s):
+    """fp32 values 0 .. 16384 ulps either side of RN(step * s)."""
+    c = np.float32(np.array([step_bits], np.uint32).view(np.float32)[0] * np.float32(s))
+    ci = int(np.array([c], np.float32).view(np.int32)[0])
+    return [ci + sign * j for j in ULPS for sign in (1, -1)]
+
+
+def _planted_near_steps():
+    """Blocks whose quotients v / absmax sit 0 .. 16384 ulps either side of
+    every step, so that both the fast quotient and the exact one decide; each
+    block holds one scale's values after its absmax (element 0, sign
+    alternating)."""
+    blocks = []
+    for am, s in SCALES:
+        sel = np.array([v for sb in STEP_BITS for v in _near(sb, s)], np.int32).view(np.float32)
+        assert np.all(np.abs(sel) <= np.float32(am))
+        for i in range(0, sel.size, 63):
+            blk = np.zeros(64, np.float32)
+            blk[0] = am if (i // 63) % 2 == 0 else -am
+            chunk = sel[i:i + 63]
+            blk[1:1 + chunk.size] = chunk
+            blocks.append(blk)
+    return np.concatenate(blocks)
+
+
+def test_quantize_near_steps_bit_exact():
+    x = _planted_near_steps()
+    pk_ref, am_ref = oracle.quantize_nf4(x)
+    # The planted set straddles the steps: every code occurs (checks the test).
+    codes = np.empty(x.size, np.uint8)
+    codes[0::2], codes[1::2] = pk_ref >> 4, pk_ref & 15
+    assert set(range(16)) <= set(codes.tolist())
+    r = nf4.quantize_nf4(_dev(x))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(r.packed.cpu().numpy(), pk_ref)
+    np.testing.assert_array_equal(r.absmax.cpu().numpy().view(np.uint32), am_ref.view(np.uint32))
+    # The fused double-quant kernel runs the same lane code.
+    w = nf4.quantize_weight(_dev(x), double_quant=True, dq_group=4)
+    q_ref, s_ref = oracle.dq_encode(am_ref, 4)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(w.packed.cpu().numpy(), pk_ref)
+    np.testing.assert_array_equal(w.absmax_q.cpu().numpy(), q_ref)
+    np.testing.assert_array_equal(w.absmax_scale.cpu().numpy().view(np.uint32),
+                                  s_ref.view(np.uint32))
+
+
+def test_quantize_non_finite():
+    # NaN anywhere in a block: absmax NaN, every code of the block 0 (argmin
+    # over NaN distances); +-inf: absmax inf, inf/inf = NaN -> 0, finite/inf
+    # = 0 -> code 7.
+    x = oracle.gen_normal(11, 64 * 12 + 40, 0.02)
+    x[5] = np.nan
+    x[64] = np.inf
+    x[128 + 7] = -np.inf
+    x[192 + 1], x[192 + 2] = np.inf, -np.inf
+    x[256 + 3], x[256 + 9] = np.nan, np.inf
+    x[320:384] = np.nan
+    x[64 * 12 + 39] = np.nan                     # in the partial last block
+    pk_ref, am_ref = oracle.quantize_nf4(x)
+    for dt in (torch.float32, torch.bfloat16):
+        t = _dev(x).to(dt)
+        ref_in = t.float().cpu().numpy()
+        pk_r, am_r = oracle.quantize_nf4(ref_in)
+        r = nf4.quantize_nf4(t)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(r.packed.cpu().numpy(), pk_r)
+        got = r.absmax.cpu().numpy()
+        assert np.array_equal(np.isnan(got), np.isnan(am_r))
+        np.testing.assert_array_equal(got[~np.isnan(got)].view(np.uint32),
+                                      am_r[~np.isnan(am_r)].view(np.uint32))
+    assert np.isnan(am_ref[0]) and np.isinf(am_ref[1])
+
+
+@pytest.mark.parametrize("x_off,p_off", [(1, 0), (2, 0), (3, 0), (0, 1), (0, 2), (0, 3), (5, 3)])
+def test_quantize_unaligned_views(x_off, p_off):
+    # Inputs and packed outputs at offsets that rule out 16-byte loads and
+    # 4-byte stores: the kernels' element-wise path, same results.
+    n = 64 * 37 + 29
+    x = oracle.gen_normal(300 + x_off + 7 * p_off, n, 0.02)
+    pk_ref, am_ref = oracle.quantize_nf4(x)
+    nb = -(-n // 64)
+    for bf16 in (False, True):
+        dt = torch.bfloat16 if bf16 else torch.float32
+        src = _dev(x).to(dt)
+        ref_in = src.float().cpu().numpy()
+        pk_r, am_r = oracle.quantize_nf4(ref_in) if bf16 else (pk_ref, am_ref)
+        xb = torch.zeros(n + x_off, dtype=dt, device=DEV)
+        xb[x_off:] = src
+        pb = torch.zeros((n + 1) // 2 + p_off, dtype=torch.uint8, device=DEV)
+        am = torch.empty(nb, dtype=torch.float32, device=DEV)
+        nf4._quantize_into(xb[x_off:], 64, pb[p_off:], am)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(pb[p_off:].cpu().numpy(), pk_r)
+        np.testing.assert_array_equal(am.cpu().numpy().view(np.uint32), am_r.view(np.uint32))
+        assert int(pb[:p_off].sum()) == 0
+        q = torch.empty(nb, dtype=torch.uint8, device=DEV)
+        sc = torch.empty(-(-nb // 8), dtype=torch.float32, device=DEV)
+        pb.zero_()
+        nf4._quantize_dq_into(xb[x_off:], 8, pb[p_off:], q, sc)
+        q_ref, s_ref = oracle.dq_encode(am_r, 8)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(pb[p_off:].cpu().numpy(), pk_r)
+        np.testing.assert_array_equal(q.cpu().numpy(), q_ref)
+        np.testing.assert_array_equal(sc.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
