@@ -78,13 +78,19 @@ __constant__ uint32_t kStepBits[15] = {
     0x3e9582d5u, 0x3ec753fau, 0x3f006d04u, 0x3f248db0u, 0x3f5c89dau,
 };
 
-// Lookup: bucket i = floor(16 q + 16) covers q in [-1 + i/16, -1 + (i+1)/16);
-// consecutive steps are >= 0.08 apart, so a bucket holds at most one, and
-// every step is >= 0.0016 from every bucket edge, so an index that rounding
-// puts in the neighbouring bucket still counts the same steps.  Entry i =
-// {that step's bits (+inf if none), number of steps below the bucket}; the
-// code is base + (q >= step).  Bucket 32 (q = 1) has base 15.
+// Lookup: bucket i covers q in [-1 + i/16, -1 + (i+1)/16), i = 0 .. 32
+// (bucket 32 is q = 1).  Consecutive steps are >= 0.08 apart, so a bucket
+// holds at most one; entry i = {that step's bits (+inf if none), number of
+// steps below the bucket}, and the code is base + (q >= step).
+// The bucket comes from f = RN(q + 98304): f's ulp is 2^-7, so the low 11
+// bits of f's pattern hold round(128 q) mod 2048, and those bits with the
+// low 3 cleared are 8 (i - 16) mod 2048, the byte address of entry i in a
+// 2 KB table.  Rounding moves q by <= 2^-8 and never down across an edge
+// (edges are multiples of 2^-7); up across one only from q within 2^-8 below
+// it, and no step lies within 0.0047 below an edge, so the entry counts the
+// same steps as q's own bucket.
 constexpr int kBuckets = 33;
+constexpr int kStepTableWords = 256;  // 2 KB of uint2, 33 entries used
 
 __device__ __forceinline__ void init_step_table(uint2 *tab) {
   const int i = (int)threadIdx.x;
@@ -97,89 +103,102 @@ __device__ __forceinline__ void init_step_table(uint2 *tab) {
       base += (t < lo) ? 1u : 0u;
       if (t >= lo && t < hi) step = kStepBits[k];
     }
-    tab[i] = make_uint2(step, base);
+    tab[(i - 16) & (kStepTableWords - 1)] = make_uint2(step, base);
   }
 }
 
-// Fast quotients q' = v * RN(1/s) are within 1.5 ulp + 2^-24 |q| < 2^-23 of
-// v / s, and the exact RN(v / s) within 2^-25 of it, so q' and RN(v / s) can
-// only fall on different sides of a step lying within 2^-22 of q'.  Every
-// q' within kMargin of its bucket's step marks the lane for the exact
-// quotient (the bucket's step is the only one within 0.0016 of q').
+// Fast quotients q' = v * rcp(s) (v_rcp_f32, documented to 1 ulp; s in
+// [1e-8, 2^126), so rcp(s) is a normal number) are within 2 ulp + 2^-24 |q|
+// of v / s, under 2^-22 for |q| <= 1, and the exact RN(v / s) is within
+// 2^-25 of v / s: q' and RN(v / s) can only fall on different sides of a
+// step lying within 2^-21 of q'.  A lane with any q' within kMargin of its
+// bucket's step takes the exact quotient for all 8 elements (the bucket's
+// step is the only one within 0.0016 of q').
 constexpr float kMargin = 0x1p-20f;
 
+// q in [-1 - 2^-8, 1 + 2^-8]; a NaN q reads some entry of the 2 KB table and
+// its code is never used (its lane takes the exact path).
 __device__ __forceinline__ uint32_t step_code(const uint2 *tab, float q, bool &near) {
-  q = fmaxf(q, -1.0f);  // NaN -> -1 -> code 0 (argmin over NaN distances is 0)
-  const uint32_t i = (uint32_t)__builtin_fmaf(q, 16.0f, 16.0f);  // |q| <= 1 + 2^-23: i <= 32
-  const uint2 t = tab[i];
+  const float f = q + 98304.0f;
+  const uint32_t addr = __builtin_bit_cast(uint32_t, f) & 0x7f8u;
+  const uint2 t = *(const uint2 *)((const char *)tab + addr);
   const float step = __builtin_bit_cast(float, t.x);
   near |= fabsf(q - step) <= kMargin;
   return t.y + ((q >= step) ? 1u : 0u);
 }
 
-// The lane's 8 elements e0 .. e0+7, zero past `lim` (quantizer.py:30-32).
-template <typename T, bool kVec>
-__device__ __forceinline__ void load8(const T *__restrict__ x, int64_t lim, int64_t e0,
-                                      float v[8]) {
-  if (kVec && e0 + 8 <= lim) {
-    if constexpr (sizeof(T) == 4) {
-      // Elements go through scalar temporaries: hipcc folds a bit_cast of a
-      // vector-element subscript to element 0 for every index.
-      const u32x4 a = *(const u32x4 *)(x + e0);
-      const u32x4 b = *(const u32x4 *)(x + e0 + 4);
+// The lane's 8 elements e0 .. e0+7 (all below the limit): 16-byte loads.
+template <typename T>
+__device__ __forceinline__ void load8_full(const T *__restrict__ x, int64_t e0, float v[8]) {
+  // Elements go through scalar temporaries: hipcc folds a bit_cast of a
+  // vector-element subscript to element 0 for every index.
+  if constexpr (sizeof(T) == 4) {
+    const u32x4 a = *(const u32x4 *)(x + e0);
+    const u32x4 b = *(const u32x4 *)(x + e0 + 4);
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const uint32_t ak = a[k], bk = b[k];
-        v[k] = __builtin_bit_cast(float, ak);
-        v[4 + k] = __builtin_bit_cast(float, bk);
-      }
-    } else {
-      const u32x4 a = *(const u32x4 *)(x + e0);
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const uint32_t ak = a[k];
-        v[2 * k] = __builtin_bit_cast(float, ak << 16);
-        v[2 * k + 1] = __builtin_bit_cast(float, ak & 0xffff0000u);
-      }
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t ak = a[k], bk = b[k];
+      v[k] = __builtin_bit_cast(float, ak);
+      v[4 + k] = __builtin_bit_cast(float, bk);
     }
   } else {
+    const u32x4 a = *(const u32x4 *)(x + e0);
 #pragma unroll
-    for (int k = 0; k < 8; ++k) v[k] = (e0 + k < lim) ? load_elem<T>(x, e0 + k) : 0.0f;
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t ak = a[k];
+      v[2 * k] = __builtin_bit_cast(float, ak << 16);
+      v[2 * k + 1] = __builtin_bit_cast(float, ak & 0xffff0000u);
+    }
   }
 }
 
-// max(m, m of the lane that DPP control kCtrl names), NaN-propagating.
+// The lane's 8 elements, each loaded on its own, zero past `lim`
+// (quantizer.py:30-32): any alignment, any tail.
+template <typename T>
+__device__ __forceinline__ void load8_guarded(const T *__restrict__ x, int64_t lim, int64_t e0,
+                                              float v[8]) {
+#pragma unroll
+  for (int k = 0; k < 8; ++k) v[k] = (e0 + k < lim) ? load_elem<T>(x, e0 + k) : 0.0f;
+}
+
+// Unsigned max of m and m of the lane that DPP control kCtrl names.
 template <int kCtrl>
-__device__ __forceinline__ float dpp_max(float m) {
-  const int o = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, m), kCtrl, 0xF, 0xF, false);
-  return __builtin_elementwise_maximum(m, __builtin_bit_cast(float, o));
+__device__ __forceinline__ uint32_t dpp_umax(uint32_t m) {
+  const uint32_t o = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, kCtrl, 0xF, 0xF, false);
+  return (o > m) ? o : m;
 }
 
 // Codes of the lane's 8 elements, packed as quantizer.py:43-46 packs them
 // (even element in the high nibble), and the block's unclamped absmax
 // (:35, :48-53) in every lane of the block.  Call with the whole wave
 // active: the absmax is reduced across the block's 8 lanes with DPP moves
-// (quad xor 1, quad xor 2, half-row mirror).
+// (quad xor 1, quad xor 2, half-row mirror) on the bit patterns of |x|,
+// whose unsigned order is the numeric order with NaN above +inf (torch's
+// max propagates NaN).
+template <bool kFull>
 __device__ __forceinline__ float encode8(const uint2 *tab, const float v[8], int64_t e0,
                                          int64_t lim, uint32_t &word) {
-  float m = __builtin_elementwise_maximum(fabsf(v[0]), fabsf(v[1]));  // NaN-propagating, :35
+  float ml = __builtin_elementwise_maximum(fabsf(v[0]), fabsf(v[1]));  // NaN-propagating
 #pragma unroll
-  for (int k = 2; k < 8; ++k) m = __builtin_elementwise_maximum(m, fabsf(v[k]));
-  m = dpp_max<0xB1>(m);   // quad_perm [1,0,3,2]
-  m = dpp_max<0x4E>(m);   // quad_perm [2,3,0,1]
-  m = dpp_max<0x141>(m);  // row_half_mirror: lane i <-> 7-i within 8
-  const float s = (m < 1e-8f) ? 1e-8f : m;  // clamp(min=1e-8), :36 (NaN stays NaN)
-  const float y = 1.0f / s;                 // correctly rounded
+  for (int k = 2; k < 8; ++k) ml = __builtin_elementwise_maximum(ml, fabsf(v[k]));
+  uint32_t mb = __builtin_bit_cast(uint32_t, ml);
+  mb = dpp_umax<0xB1>(mb);   // quad_perm [1,0,3,2]
+  mb = dpp_umax<0x4E>(mb);   // quad_perm [2,3,0,1]
+  mb = dpp_umax<0x141>(mb);  // row_half_mirror: lane i <-> 7-i within 8
+  const float m = __builtin_bit_cast(float, mb);
   uint32_t c[8];
-  bool near = false;
+  // NaN, inf and absmax >= 2^126 (rcp would be subnormal) take the exact path.
+  bool near = !(m < 0x1p126f);
+  const float y = __builtin_amdgcn_rcpf(fmaxf(m, 1e-8f));
 #pragma unroll
   for (int k = 0; k < 8; ++k) c[k] = step_code(tab, v[k] * y, near);
-  if (near) {  // rare: redo the lane with the correctly rounded quotient, :38
+  if (near) {  // rare: the correctly rounded quotient, :36-38
+    const float s = (m < 1e-8f) ? 1e-8f : m;  // clamp(min=1e-8); NaN stays NaN
     bool unused = false;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) c[k] = step_code(tab, v[k] / s, unused);
+    for (int k = 0; k < 8; ++k) c[k] = step_code(tab, fmaxf(v[k] / s, -1.0f), unused);
   }
-  if (e0 + 8 > lim) {
+  if (!kFull && e0 + 8 > lim) {
 #pragma unroll
     for (int k = 0; k < 8; ++k)
       if (e0 + k >= lim) c[k] = 0;  // odd-count pad nibble, :44-45
@@ -190,50 +209,117 @@ __device__ __forceinline__ float encode8(const uint2 *tab, const float v[8], int
   return m;
 }
 
-// Bytes e0/2 .. e0/2+3 of the packed output, those below ceil(lim/2).
-template <bool kVec>
-__device__ __forceinline__ void store_codes(uint8_t *__restrict__ packed, int64_t e0,
-                                            int64_t lim, uint32_t word) {
-  if (kVec && e0 + 8 <= lim) {
-    *(uint32_t *)(packed + (e0 >> 1)) = word;
-  } else {
+// A tile is 8 blocks (512 elements) by one wave; lane l holds elements
+// 8l .. 8l+7 of it, so the wave reads 2 KB (fp32) and writes 256 B
+// contiguously.  tile_e0(t) is the first element of tile t and
+// absmax_out(t, j, m) takes block j of tile t.
+
+// One tile with every access guarded: elements at or past `lim` read as
+// absent and are not written (the last, partial tile; unaligned buffers).
+template <typename T, typename AbsmaxOut>
+__device__ __forceinline__ void quantize_tile_guarded(const T *__restrict__ x, int64_t lim,
+                                                      int64_t t, int64_t tile_e0,
+                                                      const uint2 *tab,
+                                                      uint8_t *__restrict__ packed,
+                                                      AbsmaxOut absmax_out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t e0 = tile_e0 + 8 * lane;
+  float v[8];
+  load8_guarded<T>(x, lim, e0, v);
+  uint32_t word;
+  const float m = encode8<false>(tab, v, e0, lim, word);
+  if (e0 < lim) {
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       if (e0 + 2 * j < lim) packed[(e0 >> 1) + j] = (uint8_t)(word >> (8 * j));
+    if ((lane & 7) == 0) absmax_out(t, lane >> 3, m);
   }
 }
 
-// A tile is 8 blocks (512 elements) by one wave; lane l holds elements
-// 8l .. 8l+7, so the wave reads 2 KB and writes 256 B contiguously.  Each
-// wave takes kU consecutive tiles per pass (loads of all kU issued first).
+// Chunks of kU full tiles (x 16-byte and packed 4-byte aligned): one wave
+// takes chunks c0, c0 + dc, ... < nchunks, with the next chunk's loads
+// issued before the current chunk's codes (two register sets, alternating).
+// Every path through a chunk issues the same loads and stores (all 8 lanes
+// of a block store its absmax, the same value to the same address; the
+// loop's exits each get their own copy of the codes), so the wait before a
+// chunk's codes leaves the next chunk's loads and the last stores in flight.
+template <typename T, int kU, typename TileE0, typename AbsmaxOut>
+__device__ __forceinline__ void quantize_wave_full(const T *__restrict__ x, int64_t nchunks,
+                                                   int64_t c0, int64_t dc, const uint2 *tab,
+                                                   uint8_t *__restrict__ packed, TileE0 tile_e0,
+                                                   AbsmaxOut absmax_out) {
+  const int lane = threadIdx.x & 63;
+  if (c0 >= nchunks) return;  // wave-uniform
+  float va[kU][8], vb[kU][8];
+  auto load = [&](float (&v)[kU][8], int64_t c) {
+#pragma unroll
+    for (int u = 0; u < kU; ++u) load8_full<T>(x, tile_e0(c * kU + u) + 8 * lane, v[u]);
+  };
+  auto emit = [&](float (&v)[kU][8], int64_t c) {
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int64_t t = c * kU + u;
+      const int64_t e0 = tile_e0(t) + 8 * lane;
+      uint32_t word;
+      const float m = encode8<true>(tab, v[u], e0, 0, word);
+      *(uint32_t *)(packed + (e0 >> 1)) = word;
+      absmax_out(t, lane >> 3, m);
+    }
+  };
+  load(va, c0);
+  for (int64_t c = c0;;) {
+    const int64_t cb = c + dc;
+    if (cb >= nchunks) {  // wave-uniform
+      emit(va, c);
+      break;
+    }
+    load(vb, cb);
+    emit(va, c);
+    const int64_t ca = cb + dc;
+    if (ca >= nchunks) {
+      emit(vb, cb);
+      break;
+    }
+    load(va, ca);
+    emit(vb, cb);
+    c = ca;
+  }
+}
+
+// Tiles 0 .. ntiles-1 of a range whose elements end at `lim`, by wave `wid`
+// of `nw`: whole chunks of full tiles through the pipelined path when kVec,
+// the rest (the partial last tile, full tiles short of a chunk, every tile
+// when !kVec) guarded.
+template <typename T, bool kVec, int kU, typename TileE0, typename AbsmaxOut>
+__device__ __forceinline__ void quantize_range(const T *__restrict__ x, int64_t lim,
+                                               int64_t ntiles, int64_t wid, int64_t nw,
+                                               const uint2 *tab, uint8_t *__restrict__ packed,
+                                               TileE0 tile_e0, AbsmaxOut absmax_out) {
+  int64_t t0 = 0;
+  if (kVec) {
+    const int64_t nfull = (tile_e0(ntiles - 1) + 512 <= lim) ? ntiles : ntiles - 1;
+    const int64_t nchunks = nfull / kU;
+    quantize_wave_full<T, kU>(x, nchunks, wid, nw, tab, packed, tile_e0, absmax_out);
+    t0 = nchunks * kU;
+  }
+  for (int64_t t = t0 + wid; t < ntiles; t += nw)
+    quantize_tile_guarded<T>(x, lim, t, tile_e0(t), tab, packed, absmax_out);
+}
+
 // kVec: x 16-byte and packed 4-byte aligned (16-byte loads, 4-byte stores).
 template <typename T, bool kVec, int kU>
 __global__ void __launch_bounds__(256) quantize64_kernel(const T *__restrict__ x, int64_t n,
                                                          uint8_t *__restrict__ packed,
                                                          float *__restrict__ absmax,
                                                          int64_t ntiles) {
-  __shared__ uint2 tab[kBuckets];
+  __shared__ uint2 tab[kStepTableWords];
   init_step_table(tab);
   __syncthreads();
-  const int lane = threadIdx.x & 63;
-  const int64_t nwaves = (int64_t)gridDim.x * 4;
-  for (int64_t w = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); w * kU < ntiles; w += nwaves) {
-    float v[kU][8];
-#pragma unroll
-    for (int u = 0; u < kU; ++u) load8<T, kVec>(x, n, (w * kU + u) * 512 + 8 * lane, v[u]);
-#pragma unroll
-    for (int u = 0; u < kU; ++u) {
-      const int64_t t = w * kU + u;
-      if (t >= ntiles) break;  // wave-uniform
-      const int64_t e0 = t * 512 + 8 * lane;
-      uint32_t word;
-      const float m = encode8(tab, v[u], e0, n, word);
-      if (e0 < n) {
-        store_codes<kVec>(packed, e0, n, word);
-        if ((lane & 7) == 0) absmax[t * 8 + (lane >> 3)] = m;  // :48-53, unclamped
-      }
-    }
-  }
+  quantize_range<T, kVec, kU>(
+      x, n, ntiles, (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6),
+      (int64_t)gridDim.x * 4, tab,
+      packed, [](int64_t t) { return t * 512; },
+      [=](int64_t t, int j, float m) { absmax[t * 8 + j] = m; });  // :48-53, unclamped
 }
 
 // Any block size: per-block absmax, then per-byte codes.
@@ -327,7 +413,7 @@ __global__ void __launch_bounds__(256) quantize_dq_kernel(const T *__restrict__ 
                                                           float *__restrict__ scale,
                                                           int64_t nblocks) {
   extern __shared__ float am_lds[];  // `group` block absmax
-  __shared__ uint2 tab[kBuckets];
+  __shared__ uint2 tab[kStepTableWords];
   __shared__ float red[4];
   init_step_table(tab);
   __syncthreads();
@@ -337,25 +423,10 @@ __global__ void __launch_bounds__(256) quantize_dq_kernel(const T *__restrict__ 
   // Elements of this group's blocks: the others read as absent, so a tile
   // that runs past the group (group < 8) neither counts nor writes them.
   const int64_t lim = (64 * (b0 + nb) < n) ? 64 * (b0 + nb) : n;
-  const int ntl = (int)((nb + 7) >> 3);
-  for (int w = wave; w * kU < ntl; w += 4) {
-    float v[kU][8];
-#pragma unroll
-    for (int u = 0; u < kU; ++u)
-      load8<T, kVec>(x, lim, (b0 + 8 * (w * kU + u)) * 64 + 8 * lane, v[u]);
-#pragma unroll
-    for (int u = 0; u < kU; ++u) {
-      const int t = w * kU + u;
-      if (t >= ntl) break;  // wave-uniform
-      const int64_t e0 = (b0 + 8 * t) * 64 + 8 * lane;
-      uint32_t word;
-      const float m = encode8(tab, v[u], e0, lim, word);
-      if (e0 < lim) {
-        store_codes<kVec>(packed, e0, lim, word);
-        if ((lane & 7) == 0) am_lds[8 * t + (lane >> 3)] = m;
-      }
-    }
-  }
+  quantize_range<T, kVec, kU>(
+      x, lim, (nb + 7) >> 3, __builtin_amdgcn_readfirstlane(wave), 4, tab, packed,
+      [=](int64_t t) { return (b0 + 8 * t) * 64; },
+      [=](int64_t t, int j, float m) { am_lds[8 * t + j] = m; });
   __syncthreads();
   float m = 0.0f;
   for (int64_t i = threadIdx.x; i < nb; i += blockDim.x) {
@@ -550,7 +621,8 @@ static int32_t dequant_batch(const nf4s_tensor *ts, const int64_t *ns, uint16_t 
   return NF4S_OK;
 }
 
-constexpr int kQuantU = 2;  // tiles per wave pass
+constexpr int kQuantU = 1;         // tiles per chunk
+constexpr int kQuantMaxGrid = 2048;  // workgroups of the block-64 quantize launch
 
 template <typename T>
 static bool quantize_vec_ok(const T *x, const uint8_t *packed) {
@@ -560,12 +632,13 @@ static bool quantize_vec_ok(const T *x, const uint8_t *packed) {
 template <typename T>
 static int32_t quantize64(const T *x, int64_t n, uint8_t *packed, float *absmax, hipStream_t s) {
   const int64_t ntiles = (n + 511) / 512;
-  const int grid = grid_for((ntiles + kQuantU - 1) / kQuantU, 4);
+  int64_t grid = ((ntiles + kQuantU - 1) / kQuantU + 3) / 4;
+  if (grid > kQuantMaxGrid) grid = kQuantMaxGrid;
   if (quantize_vec_ok(x, packed))
-    hipLaunchKernelGGL((quantize64_kernel<T, true, kQuantU>), dim3(grid), dim3(256), 0, s, x, n,
+    hipLaunchKernelGGL((quantize64_kernel<T, true, kQuantU>), dim3((uint32_t)grid), dim3(256), 0, s, x, n,
                        packed, absmax, ntiles);
   else
-    hipLaunchKernelGGL((quantize64_kernel<T, false, kQuantU>), dim3(grid), dim3(256), 0, s, x, n,
+    hipLaunchKernelGGL((quantize64_kernel<T, false, kQuantU>), dim3((uint32_t)grid), dim3(256), 0, s, x, n,
                        packed, absmax, ntiles);
   return check_launch("quantize64_kernel");
 }
