@@ -10,10 +10,13 @@
 //
 // Workgroup = 4 waves in 2 x 2, tile = 256 dW rows (n) x 256 dW columns (k);
 // each wave owns 128 x 128 in 256 accumulator registers (16 tiles of
-// v_mfma_f32_32x32x16_bf16).  Per 64-token step the dy tile (64 x 256 bf16)
-// and the x tile (64 x 256) move into LDS with direct-to-LDS loads (two
-// stages of 64 KB), and each wave reads its fragments with the transposing
-// ds_read_b64_tr_b16: 8 consecutive tokens of one column per lane.
+// v_mfma_f32_32x32x16_bf16).  Per 32-token step the dy tile (32 x 256 bf16)
+// and the x tile (32 x 256) move into LDS with direct-to-LDS loads, into a
+// ring of kWgStages 32 KB stages that keeps the next kWgStages - 1 steps in
+// flight while step t computes (3 stages measured faster than 2 of 64
+// tokens, and than 4 or 5 of 32), and each wave reads its fragments with
+// the transposing ds_read_b64_tr_b16: 8 consecutive tokens of one column
+// per lane.
 #include "abi_common.hpp"
 #include "gemm_common.hpp"
 #include "nf4_device.hpp"
@@ -22,7 +25,8 @@ namespace nf4s {
 
 constexpr int kWgThreads = 256;
 constexpr int kWgTile = 256;  // dW rows and columns per workgroup
-constexpr int kWgStep = 64;   // tokens per step
+constexpr int kWgStep = 32;   // tokens per step
+constexpr int kWgStages = 3;  // LDS ring stages
 
 struct WgradArgs {
   const uint16_t *dy;  // [M, N], row stride N
@@ -56,7 +60,7 @@ __device__ __forceinline__ void wg_map_tile(const WgradArgs &g, int b, int &tn, 
   tk = bk * g.blk_k + i % g.blk_k;
 }
 
-// LDS tile: 64 token rows x 256 columns (512 B = 32 units of 16 B per row).
+// LDS tile: 32 token rows x 256 columns (512 B = 32 units of 16 B per row).
 // A wave reads one 128-column half (16 units).  Unit u of row r lives at
 // physical unit (u & 16) | ((u & 15) ^ 5 (r % 4)): with it, each 32-lane
 // half of a transposed fragment read covers 16 distinct 16-B units of one
@@ -67,8 +71,8 @@ __device__ __forceinline__ int wg_unit(int row, int u) {
   return (u & 16) | ((u & 15) ^ (5 * (row & 3)));
 }
 
-// [stage][operand 0 = dy, 1 = x][row * 32 + unit]: 2 x 2 x 32 KB.
-__shared__ u32x4 g_wg_lds[2][2][64 * 32];
+// [stage][operand 0 = dy, 1 = x][row * 32 + unit]: kWgStages x 2 x 16 KB.
+__shared__ u32x4 g_wg_lds[kWgStages][2][kWgStep * 32];
 
 // Byte offset (from its tile's base) of lane `lane`'s first transposed read
 // of fragment j: column 32j + lane % 32 of the wave's half h, token rows
@@ -108,28 +112,28 @@ __device__ __forceinline__ void wg_read(const char *tdy, const char *tx, const u
   }
 }
 
-// One 64-token step t from stage `cur`: 4 sub-steps of 16 MFMAs; the
-// fragments of sub-step s+1 are read (one per MFMA slot) during sub-step s,
-// and step t+1's 16 DMAs of this wave (8 dy rows, 8 x rows, two 256-column
-// rows per instruction) go into the other stage during sub-steps 0-1.  That
-// stage was last read in step t-1, before the barrier that ended it.  The
-// barrier after MFMA 7 of sub-step 3 waits for every DMA and LDS read; the
-// last 8 MFMAs (operands in registers) open the next call, each followed by
-// one of the next step's sub-step 0 reads.
-// `more` (no next step) skips the DMAs of the tile's last step.  As a branch
-// it splits the step into basic blocks, which keeps each DMA after its
-// slot's MFMA and reads; a single-block variant with the DMAs unconditional
-// measured 2-3 % slower on 70B shapes.
-// The four LDS tiles come in as distinct __restrict__ pointers: the
-// compiler then knows that DMAs into the next stage never alias the reads of
-// the current one and waits (vmcnt) only at the barrier.
+// One 32-token step t from stage `cur`: 2 sub-steps of 16 MFMAs.  The
+// fragments of sub-step 1 are read (one per MFMA slot) during sub-step 0.
+// The 8 DMAs of this wave for step t + kWgStages - 1 (4 dy row pairs, 4 x
+// row pairs, two 256-column rows per instruction) go into stage `nxt` after
+// MFMAs 9, 11, .., 23 (the same DMAs in sub-step 0's first half measured
+// 1-2 % slower on 70B shapes); that stage held step t-1, whose reads all
+// ended before the barrier that closed step t-1.  The caller's barrier
+// after MFMA 7 of sub-step 1 waits for step t+1's DMAs (leaving the later
+// steps' in flight) and every LDS read; the last 8 MFMAs (operands in
+// registers) open the next call, each followed by one of the next step's
+// sub-step 0 reads.
+// `more` (that step exists) is a branch around the DMAs, which keeps each
+// DMA after its slot's MFMA and reads.  The LDS stages come in as distinct
+// __restrict__ pointers: the compiler then knows that DMAs into `nxt` never
+// alias the reads of `cur` and waits (vmcnt) only at the barriers.
 __device__ __forceinline__ void wgrad_step(floatx16 (&acc)[4][4], u32x4 (&fd)[2][4],
                                            u32x4 (&fx)[2][4], const char *__restrict__ cur_dy,
                                            const char *__restrict__ cur_x,
                                            char *__restrict__ nxt_dy, char *__restrict__ nxt_x,
                                            const uint32_t (&rdy)[4], const uint32_t (&rx)[4],
                                            __amdgpu_buffer_rsrc_t rs_dy, __amdgpu_buffer_rsrc_t rs_x,
-                                           uint32_t (&vdy)[8], uint32_t (&vx)[8],
+                                           uint32_t (&vdy)[4], uint32_t (&vx)[4],
                                            uint32_t step_dy, uint32_t step_x, bool more, int wave) {
   // Previous step's last 8 MFMAs, then this step's sub-step 0 reads.
   static_for<0, 8>([&](auto I) {
@@ -141,36 +145,47 @@ __device__ __forceinline__ void wgrad_step(floatx16 (&acc)[4][4], u32x4 (&fd)[2]
     wg_read(cur_dy, cur_x, rdy, rx, fd[0], fx[0], 0, i);
     __builtin_amdgcn_sched_barrier(0);
   });
-  static_for<0, 56>([&](auto N) {
+  static_for<0, 24>([&](auto N) {
     constexpr int n = decltype(N)::value;
     constexpr int s = n / 16, i = n % 16;
     constexpr int mt = i >> 2, nt = i & 3;
     acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-        __builtin_bit_cast(bf16x8, fx[s & 1][nt]), __builtin_bit_cast(bf16x8, fd[s & 1][mt]),
+        __builtin_bit_cast(bf16x8, fx[s][nt]), __builtin_bit_cast(bf16x8, fd[s][mt]),
         acc[mt][nt], 0, 0, 0);
-    if constexpr (s < 3 && i < 8)
-      wg_read(cur_dy, cur_x, rdy, rx, fd[(s + 1) & 1], fx[(s + 1) & 1], s + 1, i);
-    if constexpr (s < 2 && (i & 1) == 1) {
-      // DMA d = 8 s + i / 2: operand d / 8, instruction d % 8 (rows 16 wave +
-      // 2 (d % 8) and the next).
-      constexpr int d = 8 * s + i / 2;
+    if constexpr (s == 0 && i < 8) wg_read(cur_dy, cur_x, rdy, rx, fd[1], fx[1], 1, i);
+    if constexpr (n >= 8 && (n & 1) == 1) {
+      // DMA d = (n - 8) / 2 after MFMAs 9, 11, .., 23: operand d / 4,
+      // instruction d % 4 (rows 8 wave + 2 (d % 4) and the next).
+      constexpr int d = (n - 8) / 2;
       if (more) {
-        if constexpr (d < 8) {
+        if constexpr (d < 4) {
           __builtin_amdgcn_raw_ptr_buffer_load_lds(
-              rs_dy, (lds_void_t *)(nxt_dy + 1024 * (8 * wave + d)), 16,
+              rs_dy, (lds_void_t *)(nxt_dy + 1024 * (4 * wave + d)), 16,
               (int)vdy[d], 0, 0, 0);
           vdy[d] += step_dy;
         } else {
           __builtin_amdgcn_raw_ptr_buffer_load_lds(
-              rs_x, (lds_void_t *)(nxt_x + 1024 * (8 * wave + d - 8)), 16, (int)vx[d - 8], 0, 0,
+              rs_x, (lds_void_t *)(nxt_x + 1024 * (4 * wave + d - 4)), 16, (int)vx[d - 4], 0, 0,
               0);
-          vx[d - 8] += step_x;
+          vx[d - 4] += step_x;
         }
       }
     }
     __builtin_amdgcn_sched_barrier(0);
   });
-  step_barrier<0>();
+}
+
+// The barrier that closes step t: this wave's DMAs of step t+1 have landed
+// and every LDS read of step t has ended.  Its DMAs of the later steps in
+// the ring (t+2 .. t+kWgStages-1, 8 each, issued after t+1's, those that
+// exist) may still be in flight: vmcnt retires in issue order.
+__device__ __forceinline__ void wgrad_close_step(int64_t t, int64_t nsteps) {
+  int64_t later = nsteps - t - 2;  // steps after t+1 that exist, clamped below
+  later = (later < 0) ? 0 : (later > kWgStages - 2) ? kWgStages - 2 : later;
+  static_for<0, kWgStages - 1>([&](auto I) {
+    constexpr int a = decltype(I)::value;  // exactly one a == later
+    if (later == a) step_barrier<8 * a>();
+  });
 }
 
 // One output tile: its 256 x 256 dW block over all M tokens.
@@ -185,10 +200,12 @@ __global__ void __launch_bounds__(kWgThreads, 1) wgrad_kernel(const WgradArgs g)
     rdy[j] = wg_read_off(lane, hn, j);
     rx[j] = wg_read_off(lane, hk, j);
   }
-  char *lds0_dy = reinterpret_cast<char *>(&g_wg_lds[0][0][0]);
-  char *lds0_x = reinterpret_cast<char *>(&g_wg_lds[0][1][0]);
-  char *lds1_dy = reinterpret_cast<char *>(&g_wg_lds[1][0][0]);
-  char *lds1_x = reinterpret_cast<char *>(&g_wg_lds[1][1][0]);
+  char *ldy[kWgStages], *lx[kWgStages];
+#pragma unroll
+  for (int i = 0; i < kWgStages; ++i) {
+    ldy[i] = reinterpret_cast<char *>(&g_wg_lds[i][0][0]);
+    lx[i] = reinterpret_cast<char *>(&g_wg_lds[i][1][0]);
+  }
   const int64_t nsteps = (g.M + kWgStep - 1) / kWgStep;
   const uint32_t step_dy = (uint32_t)(kWgStep * g.N * 2);
   const uint32_t step_x = (uint32_t)(kWgStep * g.K * 2);
@@ -205,27 +222,33 @@ __global__ void __launch_bounds__(kWgThreads, 1) wgrad_kernel(const WgradArgs g)
         (void *)(g.dy + n0), 0, (int)(g.M * g.N * 2 - n0 * 2), kBufferFlags);
     const __amdgpu_buffer_rsrc_t rs_x = __builtin_amdgcn_make_buffer_rsrc(
         (void *)(g.x + k0), 0, (int)(g.M * g.K * 2 - k0 * 2), kBufferFlags);
-    // Lane offsets of this wave's 8 DMAs per operand for step 0: instruction
-    // d writes rows 16 wave + 2d + (lane / 32), physical unit lane % 32.
-    uint32_t vdy[8], vx[8];
+    // Lane offsets of this wave's 4 DMAs per operand for step 0: instruction
+    // d writes rows 8 wave + 2d + (lane / 32), physical unit lane % 32.
+    uint32_t vdy[4], vx[4];
 #pragma unroll
-    for (int d = 0; d < 8; ++d) {
-      const int r = 16 * wave + 2 * d + (lane >> 5);
+    for (int d = 0; d < 4; ++d) {
+      const int r = 8 * wave + 2 * d + (lane >> 5);
       const int u = wg_unit(r, lane & 31);  // the logical unit stored at physical lane % 32
       vdy[d] = (uint32_t)(r * g.N * 2 + 16 * u);
       vx[d] = (uint32_t)(r * g.K * 2 + 16 * u);
     }
-    // Prologue: step 0's tiles into stage 0.
+    // Prologue: steps 0 .. kWgStages-2 (those that exist) into their
+    // stages, then wait for step 0.
 #pragma unroll
-    for (int d = 0; d < 8; ++d) {
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_dy, (lds_void_t *)(lds0_dy + 1024 * (8 * wave + d)),
-                                               16, (int)vdy[d], 0, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_x, (lds_void_t *)(lds0_x + 1024 * (8 * wave + d)),
-                                               16, (int)vx[d], 0, 0, 0);
-      vdy[d] += step_dy;
-      vx[d] += step_x;
+    for (int p = 0; p < kWgStages - 1; ++p) {
+      if (p < nsteps) {
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(
+              rs_dy, (lds_void_t *)(ldy[p] + 1024 * (4 * wave + d)), 16, (int)vdy[d], 0, 0, 0);
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(
+              rs_x, (lds_void_t *)(lx[p] + 1024 * (4 * wave + d)), 16, (int)vx[d], 0, 0, 0);
+          vdy[d] += step_dy;
+          vx[d] += step_x;
+        }
+      }
     }
-    step_barrier<0>();
+    wgrad_close_step(-1, nsteps);
 
     floatx16 acc[4][4];
 #pragma unroll
@@ -240,17 +263,28 @@ __global__ void __launch_bounds__(kWgThreads, 1) wgrad_kernel(const WgradArgs g)
       fd[1][i] = (u32x4){0u, 0u, 0u, 0u};
       fx[1][i] = (u32x4){0u, 0u, 0u, 0u};
     }
+    // Step t computes from stage t % kWgStages and loads step
+    // t + kWgStages - 1 into the stage before it.
     int64_t t = 0;
 #pragma unroll 1
-    for (; t + 2 <= nsteps; t += 2) {
-      wgrad_step(acc, fd, fx, lds0_dy, lds0_x, lds1_dy, lds1_x, rdy, rx, rs_dy, rs_x, vdy, vx,
-                 step_dy, step_x, t + 1 < nsteps, wave);
-      wgrad_step(acc, fd, fx, lds1_dy, lds1_x, lds0_dy, lds0_x, rdy, rx, rs_dy, rs_x, vdy, vx,
-                 step_dy, step_x, t + 2 < nsteps, wave);
+    for (; t + kWgStages <= nsteps; t += kWgStages) {
+      static_for<0, kWgStages>([&](auto I) {
+        constexpr int i = decltype(I)::value;
+        constexpr int c = i, nx = (i + kWgStages - 1) % kWgStages;
+        wgrad_step(acc, fd, fx, ldy[c], lx[c], ldy[nx], lx[nx], rdy, rx, rs_dy, rs_x, vdy, vx,
+                   step_dy, step_x, t + i + kWgStages - 1 < nsteps, wave);
+        wgrad_close_step(t + i, nsteps);
+      });
     }
-    if (t < nsteps)
-      wgrad_step(acc, fd, fx, lds0_dy, lds0_x, lds1_dy, lds1_x, rdy, rx, rs_dy, rs_x, vdy, vx,
-                 step_dy, step_x, false, wave);
+    static_for<0, kWgStages - 1>([&](auto I) {
+      constexpr int i = decltype(I)::value;
+      constexpr int c = i, nx = (i + kWgStages - 1) % kWgStages;
+      if (t + i < nsteps) {
+        wgrad_step(acc, fd, fx, ldy[c], lx[c], ldy[nx], lx[nx], rdy, rx, rs_dy, rs_x, vdy, vx,
+                   step_dy, step_x, false, wave);
+        wgrad_close_step(t + i, nsteps);
+      }
+    });
     // The last step's final 8 MFMAs.
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -316,13 +350,13 @@ static int32_t wgrad(const uint16_t *dy, const uint16_t *x, int64_t m, int64_t n
     return fail(NF4S_ERR_MISALIGNED, "dy and x must be 16-byte aligned");
   if (!aligned(dw, 4)) return fail(NF4S_ERR_MISALIGNED, "dw must be 4-byte aligned");
   // Lane offsets are 32-bit and must stay below 2^31 for every row a step
-  // addresses, including the rows past m of the last 64-token step (which
+  // addresses, including the rows past m of the last 32-token step (which
   // read as zero only while their offsets do not wrap onto real rows).
   const int64_t lim = ((int64_t)1 << 31) - 1;
-  const int64_t rows = (m + 63) / 64 * 64;
+  const int64_t rows = (m + kWgStep - 1) / kWgStep * kWgStep;
   if (rows * n * 2 > lim || rows * k * 2 > lim)
     return fail(NF4S_ERR_UNSUPPORTED_SHAPE,
-                "dy or x larger than 2 GiB with m rounded up to 64 (m=%lld n=%lld k=%lld)",
+                "dy or x larger than 2 GiB with m rounded up to 32 (m=%lld n=%lld k=%lld)",
                 (long long)m, (long long)n, (long long)k);
   WgradArgs g{};
   g.dy = dy;

@@ -139,9 +139,9 @@ def test_requantize_argument_rejection():
 
 
 def test_wgrad_rejects_offsets_past_2gib_in_the_last_step():
-    # m = 1 with n = 2^24: dy itself is 32 MiB, but the last 64-token step
-    # addresses rows up to 63, 2 GiB into dy, where 32-bit lane offsets wrap.
+    # m = 1 with n = 2^25: dy itself is 64 MiB, but the last 32-token step
+    # addresses rows up to 31, 2 GiB into dy, where 32-bit lane offsets wrap.
     lib = _lib.load()
-    rc = lib.nf4s_gemm_wgrad(0x1000, 0x2000, 1, 1 << 24, 8, 0x3000, 0, None)
+    rc = lib.nf4s_gemm_wgrad(0x1000, 0x2000, 1, 1 << 25, 8, 0x3000, 0, None)
     assert rc == _lib.NF4S_ERR_UNSUPPORTED_SHAPE
-    assert b"m rounded up to 64" in lib.nf4s_last_error_message()
+    assert b"m rounded up to 32" in lib.nf4s_last_error_message()
