@@ -31,9 +31,11 @@ hipBLASLt) of the 70B gate shape on the same box, and what an unfused path
 (dequantize the layer to bf16, then that GEMM rate) would reach on config 4.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
-                       [--workload all|dequant|gemm|stream] [--stream-layers L]
+                       [--workload all|dequant|gemm|stream|quantize] [--stream-layers L]
                        [--copy-calibration]
                        [--gemm-shape NAME [--gemm-mode fwd|dgrad|wgrad|swiglu]]
+  --workload quantize runs config 1 alone (oracle quantize on one core, then the
+  device quantize of the same matrix) and prints only its line (profiling).
   --gemm-shape times one fused GEMM (70b_q, 70b_k, 70b_gate, 70b_down, 7b_gate,
   7b_down) `steps` times after `warmup` and prints only its line (profiling);
   --gemm-mode bf16-reference times torch.matmul in bf16 on that shape instead.
@@ -85,7 +87,8 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="approximate CPU time budget of the dequant cpu_baseline sample")
-    ap.add_argument("--workload", choices=["all", "dequant", "gemm", "stream"], default="all")
+    ap.add_argument("--workload", choices=["all", "dequant", "gemm", "stream", "quantize"],
+                    default="all")
     ap.add_argument("--stream-layers", type=int, default=80,
                     help="config 5: number of 70B layers held in pinned host memory")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -699,6 +702,16 @@ def main():
     from aethelstream_amd import gemm, nf4
     if args.gemm_shape:
         bench_one_gemm(torch, nf4, gemm, args)
+        return
+    if args.workload == "quantize":
+        # Config 1 alone (the program the quantize kernel trace runs): the
+        # oracle's quantize of the matrix on one pinned core, then the device
+        # quantize of the same matrix, checked bit for bit.
+        with pinned_core() as pc:
+            leg, x1, pk1, am1 = cpu_baseline_quantize(pc.core)
+        print(json.dumps({"quantize_config1": bench_quantize_config1(torch, nf4, x1, pk1, am1,
+                                                                     args),
+                          "cpu_baseline_quantize_config1": leg}), flush=True)
         return
 
     line = {
