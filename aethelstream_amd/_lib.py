@@ -117,6 +117,7 @@ SIGNATURES = {
     "nf4s_gemm_fwd_grouped_noalloc": (_I32, [_P, _TP, ctypes.POINTER(_I64), ctypes.POINTER(_P),
                                              _I32, _I64, _I64, _P]),
     "nf4s_gemm_wgrad": (_I32, [_P, _P, _I64, _I64, _I64, _P, _I32, _P]),
+    "nf4s_gemm_wgrad_grouped": (_I32, [_P, _P, _P, _I32, _P, _I64, _I64, _I32, _P]),
     "nf4s_rmsnorm_fwd": (_I32, [_P, _P, _I64, _I64, ctypes.c_float, _P, _P, _P]),
     "nf4s_host_alloc": (_I32, [_I64, ctypes.POINTER(_P)]),
     "nf4s_host_free": (_I32, [_P]),

@@ -28,15 +28,32 @@ constexpr int kWgTile = 256;  // dW rows and columns per workgroup
 constexpr int kWgStep = 32;   // tokens per step
 constexpr int kWgStages = 3;  // LDS ring stages
 
+constexpr int kMaxWgGroups = 4;  // products per launch that share x
+
+// The products of one launch stack their dW row tiles: product i owns tile
+// rows tile0[i] .. tile0[i+1]-1 of a tiles_n x tiles_k grid.
 struct WgradArgs {
-  const uint16_t *dy;  // [M, N], row stride N
-  const uint16_t *x;   // [M, K], row stride K
-  float *dw;           // [N, K], row stride K
-  int64_t M, N, K;
+  const uint16_t *dy[kMaxWgGroups];  // [M, N_i], row stride N_i
+  float *dw[kMaxWgGroups];           // [N_i, K], row stride K
+  int64_t N[kMaxWgGroups];
+  int32_t tile0[kMaxWgGroups + 1];
+  int32_t ngroups;
+  const uint16_t *x;  // [M, K], row stride K
+  int64_t M, K;
   int32_t tiles_n, tiles_k;
   int32_t accumulate;
   int32_t blk_n, blk_k;  // XCD block of blk_n x blk_k tiles (0: map_tile order)
 };
+
+// a[i] for a wave-uniform i < kMaxWgGroups, as a chain of selects: indexing
+// the kernel-argument arrays with a variable would copy them to scratch.
+template <typename T>
+__device__ __forceinline__ T wg_pick(const T (&a)[kMaxWgGroups], int i) {
+  T v = a[0];
+#pragma unroll
+  for (int j = 1; j < kMaxWgGroups; ++j) v = (i == j) ? a[j] : v;
+  return v;
+}
 
 // Tile order of a launch whose rounds are all full (T a multiple of the
 // grid G, G / 8 slots per XCD): in round r, XCD x (workgroups b with
@@ -207,19 +224,29 @@ __global__ void __launch_bounds__(kWgThreads, 1) wgrad_kernel(const WgradArgs g)
     lx[i] = reinterpret_cast<char *>(&g_wg_lds[i][1][0]);
   }
   const int64_t nsteps = (g.M + kWgStep - 1) / kWgStep;
-  const uint32_t step_dy = (uint32_t)(kWgStep * g.N * 2);
   const uint32_t step_x = (uint32_t)(kWgStep * g.K * 2);
 #pragma unroll 1
   for (int b = blockIdx.x; b < T; b += gridDim.x) {
     int tn, tk;
     wg_map_tile(g, b, tn, tk);
-    const int64_t n0 = (int64_t)tn * kWgTile, k0 = (int64_t)tk * kWgTile;
+    // The product that owns tile row tn.
+    int gi = 0;
+#pragma unroll
+    for (int j = 1; j < kMaxWgGroups; ++j) gi += (j < g.ngroups && tn >= g.tile0[j]) ? 1 : 0;
+    const uint16_t *dy = wg_pick(g.dy, gi);
+    float *dw = wg_pick(g.dw, gi);
+    const int64_t N = wg_pick(g.N, gi);
+    int32_t t0 = g.tile0[0];
+#pragma unroll
+    for (int j = 1; j < kMaxWgGroups; ++j) t0 = (gi == j) ? g.tile0[j] : t0;
+    const int64_t n0 = (int64_t)(tn - t0) * kWgTile, k0 = (int64_t)tk * kWgTile;
+    const uint32_t step_dy = (uint32_t)(kWgStep * N * 2);
     // Buffer resources based at the tiles' first columns; num_records ends
     // at the matrix end, so token rows >= M (and the last row's columns past
     // the end) read as zero.  Columns past N or K of other rows read the next
     // row's values and only reach outputs that are never stored.
     const __amdgpu_buffer_rsrc_t rs_dy = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)(g.dy + n0), 0, (int)(g.M * g.N * 2 - n0 * 2), kBufferFlags);
+        (void *)(dy + n0), 0, (int)(g.M * N * 2 - n0 * 2), kBufferFlags);
     const __amdgpu_buffer_rsrc_t rs_x = __builtin_amdgcn_make_buffer_rsrc(
         (void *)(g.x + k0), 0, (int)(g.M * g.K * 2 - k0 * 2), kBufferFlags);
     // Lane offsets of this wave's 4 DMAs per operand for step 0: instruction
@@ -229,7 +256,7 @@ __global__ void __launch_bounds__(kWgThreads, 1) wgrad_kernel(const WgradArgs g)
     for (int d = 0; d < 4; ++d) {
       const int r = 8 * wave + 2 * d + (lane >> 5);
       const int u = wg_unit(r, lane & 31);  // the logical unit stored at physical lane % 32
-      vdy[d] = (uint32_t)(r * g.N * 2 + 16 * u);
+      vdy[d] = (uint32_t)(r * N * 2 + 16 * u);
       vx[d] = (uint32_t)(r * g.K * 2 + 16 * u);
     }
     // Prologue: steps 0 .. kWgStages-2 (those that exist) into their
@@ -298,12 +325,12 @@ __global__ void __launch_bounds__(kWgThreads, 1) wgrad_kernel(const WgradArgs g)
     // columns k = k0 + 128 hk + 32 nt + 8 j + 4 (l / 32) + i in registers
     // 4 j + i of tile [mt][nt]: four adjacent fp32 per 16-B store.
     const int jl = lane & 31, grp = lane >> 5;
-    const bool vec_ok = ((reinterpret_cast<uintptr_t>(g.dw) & 15) == 0) && ((g.K & 3) == 0);
+    const bool vec_ok = ((reinterpret_cast<uintptr_t>(dw) & 15) == 0) && ((g.K & 3) == 0);
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) {
       const int64_t n = n0 + 128 * hn + 32 * mt + jl;
-      if (n < g.N) {
-        float *row = g.dw + n * g.K;
+      if (n < N) {
+        float *row = dw + n * g.K;
 #pragma unroll
         for (int nt = 0; nt < 4; ++nt)
 #pragma unroll
@@ -335,43 +362,85 @@ __global__ void fill_zero_f32(float *__restrict__ p, int64_t n) {
     p[i] = 0.0f;
 }
 
-static int32_t wgrad(const uint16_t *dy, const uint16_t *x, int64_t m, int64_t n, int64_t k,
-                     float *dw, int32_t accumulate, hipStream_t s) {
-  if (dw == nullptr) return fail(NF4S_ERR_INVALID_ARGUMENT, "dw is NULL");
-  if (m > 0 && (dy == nullptr || x == nullptr))
-    return fail(NF4S_ERR_INVALID_ARGUMENT, "dy or x is NULL");
-  if (m < 0 || n <= 0 || k <= 0)
-    return fail(NF4S_ERR_INVALID_ARGUMENT, "bad weight-gradient shape m=%lld n=%lld k=%lld",
-                (long long)m, (long long)n, (long long)k);
-  if (n % 8 != 0 || k % 8 != 0)
-    return fail(NF4S_ERR_UNSUPPORTED_SHAPE, "weight gradient needs n %% 8 == 0 and k %% 8 == 0, "
-                "got n=%lld k=%lld", (long long)n, (long long)k);
-  if (!aligned(dy, 16) || !aligned(x, 16))
-    return fail(NF4S_ERR_MISALIGNED, "dy and x must be 16-byte aligned");
-  if (!aligned(dw, 4)) return fail(NF4S_ERR_MISALIGNED, "dw must be 4-byte aligned");
+static int32_t wgrad_grouped(const uint16_t *const *dys, const int64_t *ns, float *const *dws,
+                             int32_t count, const uint16_t *x, int64_t m, int64_t k,
+                             int32_t accumulate, hipStream_t s) {
+  if (count < 1 || count > kMaxWgGroups)
+    return fail(NF4S_ERR_INVALID_ARGUMENT, "weight-gradient product count %d outside [1, %d]",
+                count, kMaxWgGroups);
+  if (dys == nullptr || ns == nullptr || dws == nullptr)
+    return fail(NF4S_ERR_INVALID_ARGUMENT, "dys, ns or dws is NULL");
+  if (m < 0 || k <= 0)
+    return fail(NF4S_ERR_INVALID_ARGUMENT, "bad weight-gradient shape m=%lld k=%lld",
+                (long long)m, (long long)k);
+  if (k % 8 != 0)
+    return fail(NF4S_ERR_UNSUPPORTED_SHAPE, "weight gradient needs k %% 8 == 0, got k=%lld",
+                (long long)k);
+  if (m > 0 && x == nullptr) return fail(NF4S_ERR_INVALID_ARGUMENT, "x is NULL");
+  if (m > 0 && !aligned(x, 16)) return fail(NF4S_ERR_MISALIGNED, "x must be 16-byte aligned");
   // Lane offsets are 32-bit and must stay below 2^31 for every row a step
   // addresses, including the rows past m of the last 32-token step (which
   // read as zero only while their offsets do not wrap onto real rows).
   const int64_t lim = ((int64_t)1 << 31) - 1;
   const int64_t rows = (m + kWgStep - 1) / kWgStep * kWgStep;
-  if (rows * n * 2 > lim || rows * k * 2 > lim)
+  if (rows * k * 2 > lim)
     return fail(NF4S_ERR_UNSUPPORTED_SHAPE,
-                "dy or x larger than 2 GiB with m rounded up to 32 (m=%lld n=%lld k=%lld)",
-                (long long)m, (long long)n, (long long)k);
+                "x larger than 2 GiB with m rounded up to 32 (m=%lld k=%lld)", (long long)m,
+                (long long)k);
   WgradArgs g{};
-  g.dy = dy;
+  g.ngroups = count;
   g.x = x;
-  g.dw = dw;
   g.M = m;
-  g.N = n;
   g.K = k;
-  g.tiles_n = (int32_t)((n + kWgTile - 1) / kWgTile);
   g.tiles_k = (int32_t)((k + kWgTile - 1) / kWgTile);
   g.accumulate = accumulate ? 1 : 0;
-  const int64_t T = (int64_t)g.tiles_n * g.tiles_k;
+  int64_t tiles_n = 0;
+  for (int i = 0; i < count; ++i) {
+    const int64_t n = ns[i];
+    if (dws[i] == nullptr) return fail(NF4S_ERR_INVALID_ARGUMENT, "dw %d is NULL", i);
+    if (m > 0 && dys[i] == nullptr) return fail(NF4S_ERR_INVALID_ARGUMENT, "dy %d is NULL", i);
+    if (n <= 0)
+      return fail(NF4S_ERR_INVALID_ARGUMENT, "bad weight-gradient shape m=%lld n=%lld k=%lld",
+                  (long long)m, (long long)n, (long long)k);
+    if (n % 8 != 0)
+      return fail(NF4S_ERR_UNSUPPORTED_SHAPE, "weight gradient needs n %% 8 == 0 and k %% 8 == 0, "
+                  "got n=%lld k=%lld", (long long)n, (long long)k);
+    if (m > 0 && !aligned(dys[i], 16))
+      return fail(NF4S_ERR_MISALIGNED, "dy and x must be 16-byte aligned");
+    if (!aligned(dws[i], 4)) return fail(NF4S_ERR_MISALIGNED, "dw must be 4-byte aligned");
+    if (rows * n * 2 > lim)
+      return fail(NF4S_ERR_UNSUPPORTED_SHAPE,
+                  "dy or x larger than 2 GiB with m rounded up to 32 (m=%lld n=%lld k=%lld)",
+                  (long long)m, (long long)n, (long long)k);
+    g.dy[i] = dys[i];
+    g.dw[i] = dws[i];
+    g.N[i] = n;
+    g.tile0[i] = (int32_t)tiles_n;
+    tiles_n += (n + kWgTile - 1) / kWgTile;
+    if (tiles_n > 0x7fffffff) return fail(NF4S_ERR_UNSUPPORTED_SHAPE, "too many tiles");
+  }
+  for (int i = count; i <= kMaxWgGroups; ++i) g.tile0[i] = (int32_t)tiles_n;
+  g.tiles_n = (int32_t)tiles_n;
+  const int64_t T = tiles_n * g.tiles_k;
   if (T > 0x7fffffff) return fail(NF4S_ERR_UNSUPPORTED_SHAPE, "too many tiles");
+  if (m == 0) {
+    // An empty sum: dw += 0, or dw = 0 (a fill kernel rather than
+    // hipMemsetAsync, so that a caller may capture the call in a HIP graph).
+    // The main kernel's buffer bounds assume m > 0.
+    if (accumulate) return NF4S_OK;
+    for (int i = 0; i < count; ++i) {
+      const int64_t cnt = ns[i] * k;
+      const int64_t blocks = (cnt + 255) / 256;
+      hipLaunchKernelGGL(fill_zero_f32, dim3((uint32_t)(blocks < 65536 ? blocks : 65536)),
+                         dim3(256), 0, s, dws[i], cnt);
+      const int32_t rc = check_launch("fill_zero_f32");
+      if (rc != NF4S_OK) return rc;
+    }
+    return NF4S_OK;
+  }
   // XCD blocks (wg_map_tile) when every round is full: the squarest
-  // blk_n x blk_k = G / 8 that divides the tile grid.
+  // blk_n x blk_k = G / 8 that divides the tile grid (the products' tile
+  // rows stacked).
   const int64_t G = persistent_grid(T);
   if (G % 8 == 0 && T % G == 0) {
     const int S = (int)(G / 8);
@@ -387,17 +456,6 @@ static int32_t wgrad(const uint16_t *dy, const uint16_t *x, int64_t m, int64_t n
       }
     }
   }
-  if (m == 0) {
-    // An empty sum: dw += 0, or dw = 0 (a fill kernel rather than
-    // hipMemsetAsync, so that a caller may capture the call in a HIP graph).
-    // The main kernel's buffer bounds assume m > 0.
-    if (accumulate) return NF4S_OK;
-    const int64_t cnt = n * k;
-    const int64_t blocks = (cnt + 255) / 256;
-    hipLaunchKernelGGL(fill_zero_f32, dim3((uint32_t)(blocks < 65536 ? blocks : 65536)), dim3(256),
-                       0, s, dw, cnt);
-    return check_launch("fill_zero_f32");
-  }
   hipLaunchKernelGGL(wgrad_kernel, dim3((uint32_t)G), dim3(kWgThreads), 0, s, g);
   return check_launch("wgrad_kernel");
 }
@@ -411,8 +469,18 @@ extern "C" {
 int32_t nf4s_gemm_wgrad(const void *dy, const void *x, int64_t m, int64_t n, int64_t k,
                         float *dw, int32_t accumulate, void *stream) {
   clear_error();
-  return wgrad(static_cast<const uint16_t *>(dy), static_cast<const uint16_t *>(x), m, n, k, dw,
-               accumulate, as_stream(stream));
+  const uint16_t *dys[1] = {static_cast<const uint16_t *>(dy)};
+  float *dws[1] = {dw};
+  return wgrad_grouped(dys, &n, dws, 1, static_cast<const uint16_t *>(x), m, k, accumulate,
+                       as_stream(stream));
+}
+
+int32_t nf4s_gemm_wgrad_grouped(const void *const *dys, const int64_t *ns, float *const *dws,
+                                int32_t count, const void *x, int64_t m, int64_t k,
+                                int32_t accumulate, void *stream) {
+  clear_error();
+  return wgrad_grouped(reinterpret_cast<const uint16_t *const *>(dys), ns, dws, count,
+                       static_cast<const uint16_t *>(x), m, k, accumulate, as_stream(stream));
 }
 
 }  // extern "C"

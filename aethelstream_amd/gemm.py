@@ -13,6 +13,7 @@
 ``linear_dgrad_sum``    dx = sum_i dy_i . W_i, one launch and one rounding
                  (d_h1 at backward.rs:284-300, d_h2 at backward.rs:117-129).
 ``linear_wgrad``        dW = dy^T . x in fp32, the weight gradients beside them
+``linear_wgrad_grouped`` up to 4 of them sharing x in one launch
                  (backward.rs:87-93, 117-129, 160-168, 284-300).
 
 x / dy are bf16 [M, K] / [M, N] device tensors, W an :class:`Nf4Weight` of
@@ -196,6 +197,42 @@ def linear_wgrad(dy: torch.Tensor, x: torch.Tensor, out: Optional[torch.Tensor] 
                                            1 if accumulate else 0, _stream_ptr(dy)))
     return out
 
+
+
+def linear_wgrad_grouped(dys: Sequence[torch.Tensor], x: torch.Tensor,
+                         outs: Optional[Sequence[torch.Tensor]] = None,
+                         accumulate: bool = False) -> List[torch.Tensor]:
+    """dW_i = dys[i]^T . x for up to 4 products sharing x, in one launch: the
+    d_wq / d_wk / d_wv of backward.rs:284-300 (all from the attention input)
+    or d_wg / d_wu of :117-129.  Each result is bit-identical to
+    :func:`linear_wgrad` of that product."""
+    _require_cuda(x, *dys)
+    if not 1 <= len(dys) <= 4:
+        raise ValueError(f"linear_wgrad_grouped takes 1 to 4 products, got {len(dys)}")
+    if x.dtype != torch.bfloat16 or any(d.dtype != torch.bfloat16 for d in dys):
+        raise ValueError("dys and x must be bfloat16")
+    if x.dim() != 2 or any(d.dim() != 2 or d.shape[0] != x.shape[0] for d in dys):
+        raise ValueError("every dy [M, N_i] must share M with x [M, K]")
+    m, k = x.shape
+    ns = [d.shape[1] for d in dys]
+    if outs is None:
+        if accumulate:
+            raise ValueError("accumulate needs existing out tensors")
+        outs = [torch.empty(n, k, dtype=torch.float32, device=x.device) for n in ns]
+    outs = list(outs)
+    if len(outs) != len(dys):
+        raise ValueError("one out tensor per product")
+    _require_cuda(*outs)
+    for o, n in zip(outs, ns):
+        if o.dtype != torch.float32 or list(o.shape) != [n, k]:
+            raise ValueError(f"out must be float32 [{n}, {k}]")
+    c = len(dys)
+    dps = (ctypes.c_void_p * c)(*[d.data_ptr() for d in dys])
+    ops = (ctypes.c_void_p * c)(*[o.data_ptr() for o in outs])
+    nsa = (ctypes.c_int64 * c)(*ns)
+    _lib.check(_lib.load().nf4s_gemm_wgrad_grouped(dps, nsa, ops, c, x.data_ptr(), m, k,
+                                                   1 if accumulate else 0, _stream_ptr(x)))
+    return outs
 
 # Name of the reference function this replaces (math.rs:9).
 matmul_tb = linear_fwd

@@ -406,10 +406,18 @@ def bench_gemm(torch, nf4, gemm, args):
 
     # The weight gradients beside the input gradients (backward.rs:87-93,
     # 117-129, 160-168, 284-300): dW_i = dy_i^T . input_i in fp32, plain bf16
-    # GEMMs (no NF4 operand), reported apart from the NF4 path's rate.
+    # GEMMs (no NF4 operand), reported apart from the NF4 path's rate; those
+    # that share an input (q/k/v, gate/up) in one grouped launch, and all
+    # seven as single launches for comparison.
     dws = [torch.empty(w.shape[0], w.shape[1], dtype=torch.float32, device="cuda") for w in ws]
 
     def wgrad_pass():
+        gemm.linear_wgrad_grouped(dys[0:3], h, dws[0:3])     # d_wq, d_wk, d_wv
+        gemm.linear_wgrad(dys[3], h, dws[3])                 # d_wo
+        gemm.linear_wgrad_grouped(dys[4:6], h, dws[4:6])     # d_wg, d_wu
+        gemm.linear_wgrad(dys[6], hid, dws[6])               # d_wd
+
+    def wgrad_pass_single():
         for dy, a, dw in zip(dys, ins, dws):
             gemm.linear_wgrad(dy, a, dw)
 
@@ -437,6 +445,7 @@ def bench_gemm(torch, nf4, gemm, args):
 
     ms_fs = timed(torch, fwd_pass_swiglu, steps4, 1, name="config4_fwd_pass_swiglu")
     ms_w = timed(torch, wgrad_pass, steps4, 1, name="config4_wgrad_pass")
+    ms_w1 = timed(torch, wgrad_pass_single, steps4, 1, name="config4_wgrad_pass_single")
     fl_gu = 2 * 2.0 * M * 28672 * 8192
     ms_gu = timed(torch, lambda: gemm.linear_fwd_grouped(h, ws[4:6], ys[4:6]), steps4, 1,
                   name="gate_up_grouped")
@@ -504,6 +513,7 @@ def bench_gemm(torch, nf4, gemm, args):
         "gate_up_swiglu_fused_tflops": round(fl_gu / (ms_sw * 1e-3) / 1e12, 1),
         "dgrad_pass_tflops": round(fl_pass / (ms_d * 1e-3) / 1e12, 1),
         "wgrad_pass_tflops": round(fl_pass / (ms_w * 1e-3) / 1e12, 1),
+        "wgrad_pass_single_launch_tflops": round(fl_pass / (ms_w1 * 1e-3) / 1e12, 1),
         "per_matrix": per,
         "unfused_measured": {
             "op": "per pass: nf4s_dequant_batch_bf16 of the 7 weights, then torch.matmul / "

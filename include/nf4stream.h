@@ -249,11 +249,26 @@ int32_t nf4s_gemm_fwd_grouped_noalloc(const uint16_t *x, const nf4s_tensor *ws,
  * is the micro-batch sum of backward.rs:478-502.  dy [m, n] and x [m, k] are
  * row-major bf16 with n % 8 == 0 and k % 8 == 0, 16-byte aligned; dw [n, k]
  * row-major fp32.  dy and x must each be below 2 GiB with m rounded up to a
- * multiple of 64.  No NF4 operand: this is the plain bf16 GEMM the backward
+ * multiple of 32.  No NF4 operand: this is the plain bf16 GEMM the backward
  * pass needs beside the fused ones.
  */
 int32_t nf4s_gemm_wgrad(const void *dy, const void *x, int64_t m, int64_t n,
                         int64_t k, float *dw, int32_t accumulate, void *stream);
+
+/*
+ * Weight gradients of up to 4 products that share x, in one launch:
+ * dws[i][ns[i], k] (+)= dys[i]^T . x, each as nf4s_gemm_wgrad computes it
+ * (bit-identical).  Replaces the d_wq / d_wk / d_wv loops of
+ * single_layer_backward, which all read the attention input
+ * (doublepass/src/backward.rs:284-300), and d_wg / d_wu, which read the MLP
+ * input (:117-129).  The products' dW tiles share the launch's rounds, so
+ * the narrow k and v products (1024 rows on 70B) do not each leave half the
+ * GPU idle.  Requirements per product as nf4s_gemm_wgrad; count in [1, 4].
+ */
+int32_t nf4s_gemm_wgrad_grouped(const void *const *dys, const int64_t *ns,
+                                float *const *dws, int32_t count, const void *x,
+                                int64_t m, int64_t k, int32_t accumulate,
+                                void *stream);
 
 /*
  * RMSNorm forward producing the fused GEMMs' bf16 operand: for each row b of

@@ -148,6 +148,9 @@ extern "C" {
                                          stream: *mut c_void) -> i32;
     pub fn nf4s_gemm_wgrad(dy: *const c_void, x: *const c_void, m: i64, n: i64, k: i64,
                            dw: *mut f32, accumulate: i32, stream: *mut c_void) -> i32;
+    pub fn nf4s_gemm_wgrad_grouped(dys: *const *const c_void, ns: *const i64,
+                                   dws: *const *mut f32, count: i32, x: *const c_void, m: i64,
+                                   k: i64, accumulate: i32, stream: *mut c_void) -> i32;
     pub fn nf4s_rmsnorm_fwd(x: *const f32, w: *const f32, m: i64, d: i64, eps: f32, y: *mut u16,
                             rms: *mut f32, stream: *mut c_void) -> i32;
 

@@ -86,6 +86,26 @@ def test_wgrad_argument_rejection():
     assert f(0x1000, 0x1000, 1 << 20, 1024, 64, 0x1000, 0, None) == _lib.NF4S_ERR_UNSUPPORTED_SHAPE
 
 
+
+def test_wgrad_grouped_argument_rejection():
+    """nf4s_gemm_wgrad_grouped validates every product before any launch."""
+    lib = _lib.load()
+    f = lib.nf4s_gemm_wgrad_grouped
+    P = ctypes.c_void_p
+    dys = (P * 5)(*([0x1000] * 5))
+    dws = (P * 5)(*([0x1000] * 5))
+    ns = (ctypes.c_int64 * 5)(64, 64, 64, 64, 64)
+    assert f(dys, ns, dws, 0, 0x1000, 64, 64, 0, None) == _lib.NF4S_ERR_INVALID_ARGUMENT
+    assert f(dys, ns, dws, 5, 0x1000, 64, 64, 0, None) == _lib.NF4S_ERR_INVALID_ARGUMENT
+    assert f(None, ns, dws, 2, 0x1000, 64, 64, 0, None) == _lib.NF4S_ERR_INVALID_ARGUMENT
+    assert f(dys, ns, dws, 2, 0x1000, 64, 20, 0, None) == _lib.NF4S_ERR_UNSUPPORTED_SHAPE
+    bad_n = (ctypes.c_int64 * 3)(64, 12, 64)
+    assert f(dys, bad_n, dws, 3, 0x1000, 64, 64, 0, None) == _lib.NF4S_ERR_UNSUPPORTED_SHAPE
+    mis = (P * 3)(0x1000, 0x1000, 0x1008)
+    assert f(mis, ns, dws, 3, 0x1000, 64, 64, 0, None) == _lib.NF4S_ERR_MISALIGNED
+    nul = (P * 2)(0x1000, None)
+    assert f(dys, ns, nul, 2, 0x1000, 64, 64, 0, None) == _lib.NF4S_ERR_INVALID_ARGUMENT
+
 def test_fwd_workspace_size_query():
     """The split-K workspace query allocates nothing and needs no kernel.  On a
     host without a GPU the CU count reads as 256, the MI355X's."""

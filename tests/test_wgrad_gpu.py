@@ -153,3 +153,62 @@ def test_wgrad_rejects_bad_width():
     with pytest.raises(_lib.Nf4sError) as e:
         gemm.linear_wgrad(dy, x)
     assert e.value.status == _lib.NF4S_ERR_UNSUPPORTED_SHAPE
+
+
+# Grouped launches (products sharing x, backward.rs:284-300 and :117-129):
+# every product's tiles run the same code as a launch of their own, so each
+# dW must equal the single-product result bit for bit, whatever tile order
+# the stacked grid takes (ragged widths, 2-4 products, 64-tile rounds that
+# take the XCD-block order, accumulate).
+@pytest.mark.parametrize("m,ns,k,acc", [
+    (100, [264, 8, 1000], 136, False),             # ragged widths and tokens
+    (64, [8192, 4096, 4096], 2048, False),         # 64 x 8 tiles = 2 full rounds
+    (130, [512, 256, 256, 1024], 512, True),       # four products, accumulate
+    (1, [256, 256], 256, False),                   # one token
+])
+def test_wgrad_grouped_equals_single(m, ns, k, acc):
+    print(f"wgrad grouped m={m} ns={ns} k={k} acc={acc}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(m + k)
+    x = torch.randn(m, k, device=DEV, generator=g).to(torch.bfloat16)
+    dys = [torch.randn(m, n, device=DEV, generator=g).to(torch.bfloat16) for n in ns]
+    init = [torch.randn(n, k, device=DEV, generator=g) for n in ns]
+    singles = []
+    for dy, i0 in zip(dys, init):
+        out = i0.clone()
+        gemm.linear_wgrad(dy, x, out=out, accumulate=acc)
+        singles.append(out)
+    outs = [i0.clone() for i0 in init]
+    gemm.linear_wgrad_grouped(dys, x, outs=outs, accumulate=acc)
+    torch.cuda.synchronize()
+    for a, b in zip(outs, singles):
+        assert torch.equal(a, b)
+
+
+def test_wgrad_grouped_exact_on_integers():
+    # Small integers: every dW element is exact, so this pins each product's
+    # rows and columns (a product offset or a swapped dy shows up).
+    m, ns, k = 96, [2048, 256, 256], 1024
+    g = torch.Generator().manual_seed(5)
+    xi = torch.randint(-3, 4, (m, k), generator=g).float()
+    dyi = [torch.randint(-3, 4, (m, n), generator=g).float() for n in ns]
+    outs = gemm.linear_wgrad_grouped([d.to(DEV).to(torch.bfloat16) for d in dyi],
+                                     xi.to(DEV).to(torch.bfloat16))
+    torch.cuda.synchronize()
+    for d, o in zip(dyi, outs):
+        assert torch.equal(o.cpu(), (d.double().t() @ xi.double()).float())
+
+
+def test_wgrad_grouped_70b_qkv():
+    # Config 4's d_wq, d_wk, d_wv from one attention input: 40 x 32 tiles.
+    m, k = 8192, 8192
+    print(f"wgrad grouped 70b qkv m={m} k={k}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(21)
+    x = torch.randn(m, k, device=DEV, generator=g).to(torch.bfloat16)
+    dys = [torch.randn(m, n, device=DEV, generator=g).to(torch.bfloat16)
+           for n in (8192, 1024, 1024)]
+    outs = gemm.linear_wgrad_grouped(dys, x)
+    for dy, o in zip(dys, outs):
+        assert torch.equal(o, gemm.linear_wgrad(dy, x))
+    ref = dys[1].float().t().contiguous() @ x.float()
+    torch.cuda.synchronize()
+    assert float((outs[1] - ref).norm() / ref.norm()) <= TOL_SAME
