@@ -399,9 +399,10 @@ __global__ void __launch_bounds__(256) dq_encode_kernel(const float *__restrict_
 
 // Quantize + double-quant in one pass, for weights re-quantized on the device
 // after an update (FlowCast::on_weights_updated, flowcast/src/lib.rs:501-521,
-// after apply_galore_bf16_update, doublepass/src/precision.rs:187-202): one
-// workgroup per group of `group` 64-element blocks, its waves taking the
-// group's 8-block tiles in turn (the same lane code as quantize64_kernel).
+// after apply_galore_bf16_update, doublepass/src/precision.rs:187-202): each
+// workgroup takes groups of `group` 64-element blocks in turn (a grid of at
+// most kQuantMaxGrid), its waves taking a group's 8-block tiles in turn (the
+// same lane code as quantize64_kernel).
 // The block absmax stay in LDS (never written as fp32), so the call needs no
 // scratch memory; codes come from the fp32 absmax exactly as quantize64_kernel
 // computes them, and q / scale exactly as dq_encode_kernel does.
@@ -411,40 +412,45 @@ __global__ void __launch_bounds__(256) quantize_dq_kernel(const T *__restrict__ 
                                                           uint8_t *__restrict__ packed,
                                                           uint8_t *__restrict__ q,
                                                           float *__restrict__ scale,
-                                                          int64_t nblocks) {
+                                                          int64_t nblocks, int64_t ngroups) {
   extern __shared__ float am_lds[];  // `group` block absmax
   __shared__ uint2 tab[kStepTableWords];
   __shared__ float red[4];
   init_step_table(tab);
   __syncthreads();
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t b0 = (int64_t)blockIdx.x * group;
-  const int64_t nb = (b0 + group < nblocks) ? group : nblocks - b0;
-  // Elements of this group's blocks: the others read as absent, so a tile
-  // that runs past the group (group < 8) neither counts nor writes them.
-  const int64_t lim = (64 * (b0 + nb) < n) ? 64 * (b0 + nb) : n;
-  quantize_range<T, kVec, kU>(
-      x, lim, (nb + 7) >> 3, __builtin_amdgcn_readfirstlane(wave), 4, tab, packed,
-      [=](int64_t t) { return (b0 + 8 * t) * 64; },
-      [=](int64_t t, int j, float m) { am_lds[8 * t + j] = m; });
-  __syncthreads();
-  float m = 0.0f;
-  for (int64_t i = threadIdx.x; i < nb; i += blockDim.x) {
-    const float a = am_lds[i];
-    m = (a > m) ? a : m;  // NaN never wins, as in dq_encode_kernel
-  }
+  // Persistent: workgroup b takes groups b, b + grid, ...
+  for (int64_t grp = blockIdx.x; grp < ngroups; grp += gridDim.x) {
+    const int64_t b0 = grp * group;
+    const int64_t nb = (b0 + group < nblocks) ? group : nblocks - b0;
+    // Elements of this group's blocks: the others read as absent, so a tile
+    // that runs past the group (group < 8) neither counts nor writes them.
+    const int64_t lim = (64 * (b0 + nb) < n) ? 64 * (b0 + nb) : n;
+    quantize_range<T, kVec, kU>(
+        x, lim, (nb + 7) >> 3, __builtin_amdgcn_readfirstlane(wave), 4, tab, packed,
+        [=](int64_t t) { return (b0 + 8 * t) * 64; },
+        [=](int64_t t, int j, float m) { am_lds[8 * t + j] = m; });
+    __syncthreads();
+    float m = 0.0f;
+    for (int64_t i = threadIdx.x; i < nb; i += blockDim.x) {
+      const float a = am_lds[i];
+      m = (a > m) ? a : m;  // NaN never wins, as in dq_encode_kernel
+    }
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    const float o = __shfl_xor(m, off, 64);
-    m = (o > m) ? o : m;
+    for (int off = 32; off >= 1; off >>= 1) {
+      const float o = __shfl_xor(m, off, 64);
+      m = (o > m) ? o : m;
+    }
+    if (lane == 0) red[wave] = m;
+    __syncthreads();
+    float mx = red[0];
+    for (int w = 1; w < 4; ++w) mx = (red[w] > mx) ? red[w] : mx;
+    const float sc = dq_scale(mx);
+    if (threadIdx.x == 0) scale[grp] = sc;
+    for (int64_t i = threadIdx.x; i < nb; i += blockDim.x) q[b0 + i] = dq_code(am_lds[i], sc);
+    // The next group's absmax and partial maxima overwrite am_lds and red.
+    __syncthreads();
   }
-  if (lane == 0) red[wave] = m;
-  __syncthreads();
-  float mx = red[0];
-  for (int w = 1; w < 4; ++w) mx = (red[w] > mx) ? red[w] : mx;
-  const float sc = dq_scale(mx);
-  if (threadIdx.x == 0) scale[blockIdx.x] = sc;
-  for (int64_t i = threadIdx.x; i < nb; i += blockDim.x) q[b0 + i] = dq_code(am_lds[i], sc);
 }
 
 // ---------------------------------------------------------------------------
@@ -622,7 +628,7 @@ static int32_t dequant_batch(const nf4s_tensor *ts, const int64_t *ns, uint16_t 
 }
 
 constexpr int kQuantU = 1;         // tiles per chunk
-constexpr int kQuantMaxGrid = 2048;  // workgroups of the block-64 quantize launch
+constexpr int kQuantMaxGrid = 1024;  // workgroups of the block-64 quantize launches
 
 template <typename T>
 static bool quantize_vec_ok(const T *x, const uint8_t *packed) {
@@ -660,12 +666,13 @@ static int32_t quantize_dq(const T *x, int64_t n, int32_t block_size, int32_t gr
   const int64_t ng = (nb + group - 1) / group;
   if (ng > 0x7fffffff) return fail(NF4S_ERR_UNSUPPORTED_SHAPE, "too many groups");
   const size_t lds = (size_t)group * sizeof(float);
+  const uint32_t grid = (uint32_t)(ng < kQuantMaxGrid ? ng : kQuantMaxGrid);
   if (quantize_vec_ok(x, packed))
-    hipLaunchKernelGGL((quantize_dq_kernel<T, true, kQuantU>), dim3((uint32_t)ng), dim3(256), lds,
-                       as_stream(stream), x, n, group, packed, q, scale, nb);
+    hipLaunchKernelGGL((quantize_dq_kernel<T, true, kQuantU>), dim3(grid), dim3(256), lds,
+                       as_stream(stream), x, n, group, packed, q, scale, nb, ng);
   else
-    hipLaunchKernelGGL((quantize_dq_kernel<T, false, kQuantU>), dim3((uint32_t)ng), dim3(256),
-                       lds, as_stream(stream), x, n, group, packed, q, scale, nb);
+    hipLaunchKernelGGL((quantize_dq_kernel<T, false, kQuantU>), dim3(grid), dim3(256), lds,
+                       as_stream(stream), x, n, group, packed, q, scale, nb, ng);
   return check_launch("quantize_dq_kernel");
 }
 

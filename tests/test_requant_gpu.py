@@ -57,6 +57,23 @@ def test_quantize_dq_fused_vs_oracle(n, group, bf16):
     np.testing.assert_array_equal(_u32(w.absmax_scale), s_ref.view(np.uint32))
 
 
+
+@pytest.mark.parametrize("group,bf16", [(8, False), (16, True), (256, False)])
+def test_quantize_dq_more_groups_than_workgroups(group, bf16):
+    # The fused kernel's workgroups each take several groups in turn once
+    # there are more groups than its grid (at most 1024 workgroups): 3001+
+    # groups, a partial last group and a partial last block.
+    n = 64 * group * 3001 + 64 * 3 + 17 if group < 256 else 64 * 256 * 1100 + 100
+    print(f"quantize_dq many groups group={group} bf16={bf16} n={n}", flush=True)
+    t, ref_in = _values(n, 900 + group, bf16)
+    w = nf4.quantize_weight(t, double_quant=True, dq_group=group)
+    pk_ref, am_ref = oracle.quantize_nf4(ref_in)
+    q_ref, s_ref = oracle.dq_encode(am_ref, group)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(w.packed.cpu().numpy(), pk_ref)
+    np.testing.assert_array_equal(w.absmax_q.cpu().numpy(), q_ref)
+    np.testing.assert_array_equal(_u32(w.absmax_scale), s_ref.view(np.uint32))
+
 def test_fused_equals_two_launch_path():
     # The fused kernel and quantize_nf4 + dq_encode on the same device values.
     t, _ = _values(64 * 1000 + 3, 7, bf16=False)
