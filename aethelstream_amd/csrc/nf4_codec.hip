@@ -69,9 +69,9 @@ __device__ __forceinline__ float load_elem<uint16_t>(const uint16_t *x, int64_t 
 // distance to the lower code only grows and to the upper one only shrinks),
 // so it is a step function of the fp32 quotient: code(n) = #{k : n >= S_k}
 // for the 15 fp32 thresholds below (the smallest fp32 n with code(n) >= k;
-// nf4_code_steps.py derives them from the codebook, and an exhaustive CPU
-// check over every fp32 in [-1, 1] compares the step form with the 16-way
-// argmin).
+// aethelstream_amd/code_steps.py derives them from the codebook, and an
+// exhaustive CPU check over every fp32 in [-1, 1] compares the step form with
+// the 16-way argmin).
 __constant__ uint32_t kStepBits[15] = {
     0xbf591cd8u, 0xbf1c5270u, 0xbeeb847fu, 0xbeadea76u, 0xbe703cecu,
     0xbe0d38bbu, 0xbd3a7871u, 0x3d22fb00u, 0x3df64863u, 0x3e5067e1u,
@@ -108,12 +108,13 @@ __device__ __forceinline__ void init_step_table(uint2 *tab) {
 }
 
 // Fast quotients q' = v * rcp(s) (v_rcp_f32, documented to 1 ulp; s in
-// [1e-8, 2^126), so rcp(s) is a normal number) are within 2 ulp + 2^-24 |q|
-// of v / s, under 2^-22 for |q| <= 1, and the exact RN(v / s) is within
-// 2^-25 of v / s: q' and RN(v / s) can only fall on different sides of a
-// step lying within 2^-21 of q'.  A lane with any q' within kMargin of its
-// bucket's step takes the exact quotient for all 8 elements (the bucket's
-// step is the only one within 0.0016 of q').
+// [1e-8, 2^126), so rcp(s) is a normal number) are within |q| 2^-23 (rcp's
+// error) + 2^-25 (the product's rounding) < 2^-22 of v / s for |q| <= 1, and
+// the exact RN(v / s) is within 2^-25 of v / s: q' and RN(v / s) can only
+// fall on different sides of a step lying within 2^-21 of q'.  A lane with
+// any q' within kMargin (4x that) of its bucket's step takes the exact
+// quotient for all 8 elements (the bucket's step is the only one within
+// 0.0016 of q').
 constexpr float kMargin = 0x1p-20f;
 
 // q in [-1 - 2^-8, 1 + 2^-8]; a NaN q reads some entry of the 2 KB table and
