@@ -112,7 +112,7 @@ __device__ __forceinline__ void init_step_table(uint2 *tab) {
 // error) + 2^-25 (the product's rounding) < 2^-22 of v / s for |q| <= 1, and
 // the exact RN(v / s) is within 2^-25 of v / s: q' and RN(v / s) can only
 // fall on different sides of a step lying within 2^-21 of q'.  A lane with
-// any q' within kMargin (4x that) of its bucket's step takes the exact
+// any q' within kMargin (twice that) of its bucket's step takes the exact
 // quotient for all 8 elements (the bucket's step is the only one within
 // 0.0016 of q').
 constexpr float kMargin = 0x1p-20f;
