@@ -110,6 +110,10 @@ SIGNATURES = {
     "nf4s_gemm_fwd_swiglu": (_I32, [_P, _TP, _TP, _I64, _I64, _I64, _P, _P]),
     "nf4s_gemm_dgrad_sum": (_I32, [ctypes.POINTER(_P), _TP, ctypes.POINTER(_I64), _I32, _I64,
                                    _I64, _P, _P]),
+    "nf4s_gemm_dgrad_sum_ws": (_I32, [ctypes.POINTER(_P), _TP, ctypes.POINTER(_I64), _I32, _I64,
+                                      _I64, _P, _P, _I64, _P]),
+    "nf4s_gemm_dgrad_workspace_size": (_I32, [ctypes.POINTER(_I64), _I32, _I64, _I64,
+                                              ctypes.POINTER(_I64)]),
     "nf4s_gemm_fwd_grouped_ws": (_I32, [_P, _TP, ctypes.POINTER(_I64), ctypes.POINTER(_P), _I32,
                                         _I64, _I64, _P, _I64, _P]),
     "nf4s_gemm_fwd_workspace_size": (_I32, [ctypes.POINTER(_I64), _I32, _I64, _I64,

@@ -437,8 +437,9 @@ struct DgradProducer : DgradStore, PerStepLoads<kDQ, DgradProducer<kDQ>> {
     const int r = threadIdx.x >> 2, q = threadIdx.x & 3;
     const int64_t col = o0 + 32 * q;
     const int64_t cc = col < g.wk ? col : 0;
-    ptr = g.packed + (int64_t)r * (g.wk >> 1) + (cc >> 1);
-    am_idx = (int64_t)r * (g.wk >> 6) + (cc >> 6);
+    const int64_t row = r + 64 * g.k0;  // a split-K slice starts at W row 64 k0
+    ptr = g.packed + row * (g.wk >> 1) + (cc >> 1);
+    am_idx = row * (g.wk >> 6) + (cc >> 6);  // absolute block: scale groups stay aligned
     am = g.am;
   }
   __device__ __forceinline__ void load_step(const GemmArgs &g, int step, u32x4 &w,
@@ -478,9 +479,10 @@ struct DgradBatchProducer : DgradStore {
     (void)b0_lds;
     init_layout(g, o0);
     const int r = threadIdx.x >> 2, q = threadIdx.x & 3;
-    ptr = g.packed + (int64_t)r * (g.wk >> 1) + ((o0 + 32 * q) >> 1);
+    const int64_t row = r + 64 * g.k0;  // a split-K slice starts at W row 64 k0
+    ptr = g.packed + row * (g.wk >> 1) + ((o0 + 32 * q) >> 1);
     pstride = 64 * (g.wk >> 1);
-    gblk = (int64_t)(r + 64 * q) * (g.wk >> 6) + (o0 >> 6);
+    gblk = (row + 64 * q) * (g.wk >> 6) + (o0 >> 6);  // absolute block
     gstride = 256 * (g.wk >> 6);
     ngroups = (int)(g.R >> 8);
     shift = 8u * (uint32_t)(q >> 1);
@@ -1143,6 +1145,7 @@ __global__ void __launch_bounds__(kGemmThreads, 1) nf4_gemm_fwd_kernel(const Gro
 // stores them as bf16, so that 16 workgroups per tile keep every CU loading.
 constexpr int kFixupQuads = 4;
 constexpr int kFixupBlocksPerTile = 64 / kFixupQuads;
+template <bool kDgrad>
 __global__ void __launch_bounds__(kGemmThreads) nf4_gemm_fixup_kernel(const GroupedArgs ga) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
@@ -1150,7 +1153,16 @@ __global__ void __launch_bounds__(kGemmThreads) nf4_gemm_fixup_kernel(const Grou
   const int q = blockIdx.x - j * kFixupBlocksPerTile;
   GemmArgs g;
   int64_t m0, o0;
-  fwd_tile(ga, ga.full_tiles + j, g, m0, o0, wave);
+  if constexpr (kDgrad) {
+    // The input gradient's tile: rows and columns of dx (ga.base.out).
+    g = ga.base;
+    int tm, to;
+    map_tile(ga.full_tiles + j, g.tiles_m, g.tiles_o, tm, to);
+    m0 = (int64_t)tm * kTileM + wave * 128;
+    o0 = (int64_t)to * kTileO;
+  } else {
+    fwd_tile(ga, ga.full_tiles + j, g, m0, o0, wave);
+  }
   const bool vec_ok = ((reinterpret_cast<uintptr_t>(g.out) & 7) == 0) && ((g.ldo & 3) == 0);
   const floatx4 *part = reinterpret_cast<const floatx4 *>(ga.ws + (int64_t)j * ga.splits *
                                                                       kPartialFloats) +
@@ -1313,39 +1325,102 @@ __global__ void __launch_bounds__(kGemmThreads, 1) nf4_gemm_swiglu_kernel(const 
 // Input gradient: dx = sum_i dy_i . W_i, the groups run one after another
 // into the same accumulator.  Between two groups no barrier is needed: every
 // read of the shared weight tiles ended before the last step's barrier, and
-// the activation buffers are per wave.
-template <class Producer>
+// the activation buffers are per wave.  The reduction of a tile is the
+// groups' steps in order (group i's W rows 64 s .. 64 s + 63 at step s).
+// Work unit b < full_tiles is tile b; the units after it are split-K slices
+// of the remaining tiles (slice = unit % splits), each over split_steps of
+// that step sequence (its part of each group it meets), whose fp32 partials
+// go to the workspace and are summed by nf4_gemm_fixup_kernel<true>.  The
+// launch without a split runs the kSplit = false instantiation, which keeps
+// none of the slice bookkeeping (the split one spills a few registers per
+// tile).
+template <class Producer, bool kSplit>
 __global__ void __launch_bounds__(kGemmThreads, 1) nf4_gemm_dgrad_kernel(const GroupedArgs ga) {
   const int T = ga.base.tiles_m * ga.base.tiles_o;
+  const int U = kSplit ? ga.full_tiles + (T - ga.full_tiles) * ga.splits : T;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int jl = lane & 31;
   const int grp = lane >> 5;
+  // Reduction steps over all groups (check_offsets bounds each group's below
+  // 2^16).
+  int total = 0;
+  if constexpr (kSplit)
+    for (int gi = 0; gi < ga.ngroups; ++gi) total += (int)(ga.grp[gi].wn / kStep);
 #pragma unroll 1
-  for (int b = blockIdx.x; b < T; b += gridDim.x) {
+  for (int b = blockIdx.x; b < U; b += gridDim.x) {
+    int tile = b, slice = -1;
+    if (kSplit && b >= ga.full_tiles) {
+      const int u = b - ga.full_tiles;
+      tile = ga.full_tiles + u / ga.splits;
+      slice = u - (u / ga.splits) * ga.splits;
+    }
     GemmArgs g = ga.base;
     int tm, to;
-    map_tile(b, g.tiles_m, g.tiles_o, tm, to);
+    map_tile(tile, g.tiles_m, g.tiles_o, tm, to);
     const int64_t m0 = (int64_t)tm * kTileM + wave * 128;
     const int64_t o0 = (int64_t)to * kTileO;
     floatx16 acc[4][4];
     zero_acc(acc);
+    if constexpr (!kSplit) {
 #pragma unroll 1
-    for (int gi = 0; gi < ga.ngroups; ++gi) {
-      g.a = ga.grp[gi].a;
-      g.lda = ga.grp[gi].lda;
-      g.packed = ga.grp[gi].packed;
-      g.am = ga.grp[gi].am;
-      g.wn = ga.grp[gi].wn;
-      g.R = ga.grp[gi].wn;
-      uint32_t aoff[16];
-      const __amdgpu_buffer_rsrc_t arsrc = activation_setup(g, m0, lane, aoff);
-      Producer prod;
-      prod.init(g, o0, (uint32_t)(uintptr_t)(lds_void_t *)&g_lds_b[0][0]);
-      gemm_main<Producer>(g, prod, acc, &g_lds_a[wave][0][0], &g_lds_a[wave][1][0], g_lds_b[0],
-                          g_lds_b[1], arsrc, aoff, (int)(g.R / kStep), jl, grp);
+      for (int gi = 0; gi < ga.ngroups; ++gi) {
+        g.a = ga.grp[gi].a;
+        g.lda = ga.grp[gi].lda;
+        g.packed = ga.grp[gi].packed;
+        g.am = ga.grp[gi].am;
+        g.wn = ga.grp[gi].wn;
+        g.R = ga.grp[gi].wn;
+        uint32_t aoff[16];
+        const __amdgpu_buffer_rsrc_t arsrc = activation_setup(g, m0, lane, aoff);
+        Producer prod;
+        prod.init(g, o0, (uint32_t)(uintptr_t)(lds_void_t *)&g_lds_b[0][0]);
+        gemm_main<Producer>(g, prod, acc, &g_lds_a[wave][0][0], &g_lds_a[wave][1][0],
+                            g_lds_b[0], g_lds_b[1], arsrc, aoff, (int)(g.R / kStep), jl, grp);
+      }
+      epilogue(g, acc, wave, m0, o0, lane);
+    } else {
+      int s_lo = 0, s_hi = total;
+      if (slice >= 0) {
+        s_lo = slice * ga.split_steps;
+        s_hi = (s_lo + ga.split_steps < total) ? s_lo + ga.split_steps : total;
+      }
+      int gbase = 0;  // first step of group gi
+#pragma unroll 1
+      for (int gi = 0; gi < ga.ngroups; ++gi) {
+        const int steps = (int)(ga.grp[gi].wn / kStep);
+        const int lo = (s_lo > gbase) ? s_lo : gbase;
+        const int hi = (s_hi < gbase + steps) ? s_hi : gbase + steps;
+        if (lo < hi) {
+          g.a = ga.grp[gi].a;
+          g.lda = ga.grp[gi].lda;
+          g.packed = ga.grp[gi].packed;
+          g.am = ga.grp[gi].am;
+          g.wn = ga.grp[gi].wn;
+          g.k0 = lo - gbase;
+          g.R = (int64_t)kStep * (hi - lo);
+          uint32_t aoff[16];
+          const __amdgpu_buffer_rsrc_t arsrc = activation_setup(g, m0, lane, aoff);
+          Producer prod;
+          prod.init(g, o0, (uint32_t)(uintptr_t)(lds_void_t *)&g_lds_b[0][0]);
+          gemm_main<Producer>(g, prod, acc, &g_lds_a[wave][0][0], &g_lds_a[wave][1][0],
+                              g_lds_b[0], g_lds_b[1], arsrc, aoff, hi - lo, jl, grp);
+        }
+        gbase += steps;
+      }
+      if (slice < 0) {
+        epilogue(g, acc, wave, m0, o0, lane);
+      } else {
+        floatx4 *part = reinterpret_cast<floatx4 *>(
+            ga.ws + (int64_t)(b - ga.full_tiles) * kPartialFloats) + threadIdx.x;
+#pragma unroll
+        for (int i = 0; i < 64; ++i) {
+          const floatx16 &a = acc[i >> 4][(i >> 2) & 3];
+          const int v = 4 * (i & 3);
+          part[i * kGemmThreads] = (floatx4){a[v], a[v + 1], a[v + 2], a[v + 3]};
+        }
+      }
     }
-    epilogue(g, acc, wave, m0, o0, lane);
   }
 }
 
@@ -1458,7 +1533,7 @@ static int32_t launch_fwd(GroupedArgs &ga, hipStream_t s, void *ws, int64_t ws_b
                      0, s, ga);
   int32_t rc = check_launch("nf4_gemm_fwd");
   if (rc == NF4S_OK && ga.splits > 1) {
-    hipLaunchKernelGGL(nf4_gemm_fixup_kernel,
+    hipLaunchKernelGGL(nf4_gemm_fixup_kernel<false>,
                        dim3((uint32_t)((T - ga.full_tiles) * kFixupBlocksPerTile)),
                        dim3(kGemmThreads), 0, s, ga);
     rc = check_launch("nf4_gemm_fixup");
@@ -1466,15 +1541,63 @@ static int32_t launch_fwd(GroupedArgs &ga, hipStream_t s, void *ws, int64_t ws_b
   return rc;
 }
 
+// Reduction steps of an input-gradient launch: its groups' steps in order.
+static int64_t dgrad_steps(const int64_t *ns, int32_t count) {
+  int64_t steps = 0;
+  for (int32_t i = 0; i < count; ++i) steps += ns[i] / kStep;
+  return steps;
+}
+
 template <class Producer>
-static int32_t launch_dgrad(const GroupedArgs &ga, hipStream_t s) {
+static int32_t launch_dgrad(GroupedArgs &ga, int64_t nsteps, hipStream_t s, void *ws,
+                            int64_t ws_bytes) {
   const int64_t T = (int64_t)ga.base.tiles_m * ga.base.tiles_o;
   if (T == 0) return NF4S_OK;
   if (T > 0x7fffffff) return fail(NF4S_ERR_UNSUPPORTED_SHAPE, "too many tiles");
-  hipLaunchKernelGGL(nf4_gemm_dgrad_kernel<Producer>, dim3(persistent_grid(T)),
-                     dim3(kGemmThreads), 0, s, ga);
-  return check_launch("nf4_gemm_dgrad");
+  ga.full_tiles = (int32_t)T;
+  ga.splits = 1;
+  ga.split_steps = 0;
+  ga.ws = nullptr;
+  const SplitPlan p = split_plan(T, nsteps, Producer::kUnroll);
+  if (ws != nullptr && p.tail_tiles > 0 && ws_bytes >= split_bytes(p)) {
+    ga.full_tiles = (int32_t)(T - p.tail_tiles);
+    ga.splits = (int32_t)p.splits;
+    ga.split_steps = (int32_t)p.split_steps;
+    ga.ws = static_cast<float *>(ws);
+  }
+  const int64_t U = ga.full_tiles + (T - ga.full_tiles) * ga.splits;
+  if (ga.splits > 1)
+    hipLaunchKernelGGL((nf4_gemm_dgrad_kernel<Producer, true>), dim3(persistent_grid(U)),
+                       dim3(kGemmThreads), 0, s, ga);
+  else
+    hipLaunchKernelGGL((nf4_gemm_dgrad_kernel<Producer, false>), dim3(persistent_grid(U)),
+                       dim3(kGemmThreads), 0, s, ga);
+  int32_t rc = check_launch("nf4_gemm_dgrad");
+  if (rc == NF4S_OK && ga.splits > 1) {
+    hipLaunchKernelGGL(nf4_gemm_fixup_kernel<true>,
+                       dim3((uint32_t)((T - ga.full_tiles) * kFixupBlocksPerTile)),
+                       dim3(kGemmThreads), 0, s, ga);
+    rc = check_launch("nf4_gemm_fixup");
+  }
+  return rc;
 }
+
+// Workspace bytes the split-K input gradient over these weights needs (0: no
+// split), for either producer's step granularity.
+static int64_t dgrad_workspace_bytes(const int64_t *ns, int32_t count, int64_t m, int64_t k) {
+  if (m <= 0 || k <= 0 || k % 64 != 0) return 0;
+  for (int32_t i = 0; i < count; ++i)
+    if (ns[i] <= 0 || ns[i] % 64 != 0) return 0;
+  const int64_t T = ((m + kTileM - 1) / kTileM) * ((k + kTileO - 1) / kTileO);
+  const int64_t steps = dgrad_steps(ns, count);
+  int64_t best = 0;
+  for (int unroll : {2, 4}) {
+    const int64_t b = split_bytes(split_plan(T, steps, unroll));
+    if (b > best) best = b;
+  }
+  return best;
+}
+
 
 // Forward over `count` weights W_i [ns[i], k] sharing x [m, k]: y_i = x . W_i^T.
 // Weights of one kind (double-quantized or not, batched loads or not) share
@@ -1583,7 +1706,8 @@ static int32_t gemm_swiglu(const uint16_t *x, const nf4s_tensor *wg, const nf4s_
 // Input gradient dx [m, k] = sum_i dy_i [m, ns[i]] . W_i [ns[i], k].
 static int32_t gemm_dgrad_groups(const uint16_t *const *dys, const nf4s_tensor *ws,
                                  const int64_t *ns, int32_t count, int64_t m, int64_t k,
-                                 uint16_t *dx, hipStream_t s) {
+                                 uint16_t *dx, hipStream_t s, void *work = nullptr,
+                                 int64_t work_bytes = 0) {
   if (count <= 0 || count > kMaxGroups)
     return fail(NF4S_ERR_INVALID_ARGUMENT, "count must be 1..%d, got %d", kMaxGroups, count);
   if (dys == nullptr || ws == nullptr || ns == nullptr)
@@ -1627,10 +1751,12 @@ static int32_t gemm_dgrad_groups(const uint16_t *const *dys, const nf4s_tensor *
     else
       batch = batch && aligned(ws[i].absmax, 8);
   }
+  const int64_t nsteps = dgrad_steps(ns, count);
   if (batch)
-    return dq ? launch_dgrad<DgradBatchProducer<true>>(ga, s)
-              : launch_dgrad<DgradBatchProducer<false>>(ga, s);
-  return dq ? launch_dgrad<DgradProducer<true>>(ga, s) : launch_dgrad<DgradProducer<false>>(ga, s);
+    return dq ? launch_dgrad<DgradBatchProducer<true>>(ga, nsteps, s, work, work_bytes)
+              : launch_dgrad<DgradBatchProducer<false>>(ga, nsteps, s, work, work_bytes);
+  return dq ? launch_dgrad<DgradProducer<true>>(ga, nsteps, s, work, work_bytes)
+            : launch_dgrad<DgradProducer<false>>(ga, nsteps, s, work, work_bytes);
 }
 
 // Workspace bytes the split-K forward over these weights needs (0: no split
@@ -1774,6 +1900,31 @@ int32_t nf4s_gemm_dgrad_sum(const uint16_t *const *dys, const nf4s_tensor *ws, c
                             int32_t count, int64_t m, int64_t k, uint16_t *dx, void *stream) {
   clear_error();
   return gemm_dgrad_groups(dys, ws, ns, count, m, k, dx, as_stream(stream));
+}
+
+int32_t nf4s_gemm_dgrad_sum_ws(const uint16_t *const *dys, const nf4s_tensor *ws,
+                               const int64_t *ns, int32_t count, int64_t m, int64_t k,
+                               uint16_t *dx, void *workspace, int64_t workspace_bytes,
+                               void *stream) {
+  clear_error();
+  if (workspace_bytes < 0)
+    return fail(NF4S_ERR_INVALID_ARGUMENT, "negative workspace size %lld",
+                (long long)workspace_bytes);
+  if (workspace != nullptr && !aligned(workspace, 16))
+    return fail(NF4S_ERR_MISALIGNED, "workspace must be 16-byte aligned");
+  return gemm_dgrad_groups(dys, ws, ns, count, m, k, dx, as_stream(stream), workspace,
+                           workspace_bytes);
+}
+
+int32_t nf4s_gemm_dgrad_workspace_size(const int64_t *ns, int32_t count, int64_t m, int64_t k,
+                                       int64_t *bytes) {
+  clear_error();
+  if (bytes == nullptr) return fail(NF4S_ERR_INVALID_ARGUMENT, "bytes is NULL");
+  *bytes = 0;
+  if (count <= 0 || count > kMaxGroups || ns == nullptr)
+    return fail(NF4S_ERR_INVALID_ARGUMENT, "count must be 1..%d with sizes", kMaxGroups);
+  *bytes = dgrad_workspace_bytes(ns, count, m, k);
+  return NF4S_OK;
 }
 
 }  // extern "C"

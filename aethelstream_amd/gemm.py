@@ -57,19 +57,44 @@ def linear_fwd(x: torch.Tensor, w: Nf4Weight, out: Optional[torch.Tensor] = None
     return out
 
 
-def linear_dgrad(dy: torch.Tensor, w: Nf4Weight,
-                 out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """dx[M, K] = dy[M, N] . W[N, K] (bf16 in/out, fp32 accumulate)."""
+def linear_dgrad(dy: torch.Tensor, w: Nf4Weight, out: Optional[torch.Tensor] = None,
+                 split_k: bool = True, workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """dx[M, K] = dy[M, N] . W[N, K] (bf16 in/out, fp32 accumulate).  With
+    ``split_k`` a last round that would leave most CUs idle (few tokens) runs
+    as split-K slices, as in :func:`linear_dgrad_sum`."""
     n, k = int(w.shape[0]), int(w.shape[1])
     _check_act(dy, n, "dy")
     m = dy.shape[0]
     if out is None:
         out = torch.empty(m, k, dtype=torch.bfloat16, device=dy.device)
     _check_act(out, k, "out")
+    if split_k and dgrad_workspace_bytes([n], m, k) > 0:
+        return linear_dgrad_sum([dy], [w], out, split_k=True, workspace=workspace)
     desc = w.descriptor()
     _lib.check(_lib.load().nf4s_gemm_dgrad(dy.data_ptr(), ctypes.byref(desc), m, n, k,
                                            out.data_ptr(), _stream_ptr(dy)))
     return out
+
+
+def dgrad_workspace_bytes(ns: Sequence[int], m: int, k: int) -> int:
+    """Workspace nf4s_gemm_dgrad_sum_ws uses for these shapes (0: no split)."""
+    arr = (ctypes.c_int64 * len(ns))(*[int(v) for v in ns])
+    out = ctypes.c_int64(0)
+    _lib.check(_lib.load().nf4s_gemm_dgrad_workspace_size(arr, len(ns), m, k, ctypes.byref(out)))
+    return int(out.value)
+
+
+def _workspace_for(need: int, workspace: Optional[torch.Tensor], ref: torch.Tensor):
+    """`workspace` if it holds `need` bytes, else a new buffer from torch's
+    caching allocator on ref's device (and stream)."""
+    if workspace is not None and workspace.device != ref.device:
+        raise ValueError("workspace must be on the operands' device")
+    if workspace is None or workspace.numel() * workspace.element_size() < need:
+        workspace = torch.empty(need, dtype=torch.uint8, device=ref.device)
+    _require_cuda(workspace)
+    if not workspace.is_contiguous():
+        raise ValueError("workspace must be contiguous")
+    return workspace
 
 
 def _descs(ws: Sequence[Nf4Weight]):
@@ -149,9 +174,14 @@ def linear_swiglu(x: torch.Tensor, w_gate: Nf4Weight, w_up: Nf4Weight,
 
 
 def linear_dgrad_sum(dys: Sequence[torch.Tensor], ws: Sequence[Nf4Weight],
-                     out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                     out: Optional[torch.Tensor] = None, split_k: bool = True,
+                     workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
     """sum_i dys[i] . W_i (1..4 weights of one k): one launch, fp32 accumulation
-    over all weights, one bf16 rounding."""
+    over all weights, one bf16 rounding.  With ``split_k`` a last round that
+    would leave most CUs idle (few tokens) runs as split-K slices of the
+    weights' concatenated reduction, whose fp32 partials go to ``workspace``
+    (by default a buffer from torch's caching allocator on out's stream) and
+    are summed in slice order by a second kernel."""
     if not 1 <= len(ws) <= 4 or len(dys) != len(ws):
         raise ValueError("linear_dgrad_sum takes 1 to 4 (dy, W) pairs")
     k = int(ws[0].shape[1])
@@ -168,8 +198,15 @@ def linear_dgrad_sum(dys: Sequence[torch.Tensor], ws: Sequence[Nf4Weight],
     ns = (ctypes.c_int64 * len(ws))(*[int(w.shape[0]) for w in ws])
     dps = (ctypes.c_void_p * len(ws))(*[d.data_ptr() for d in dys])
     descs = _descs(ws)
-    _lib.check(_lib.load().nf4s_gemm_dgrad_sum(dps, descs, ns, len(ws), m, k, out.data_ptr(),
-                                               _stream_ptr(out)))
+    need = dgrad_workspace_bytes(list(ns), m, k) if split_k else 0
+    if need > 0:
+        workspace = _workspace_for(need, workspace, out)
+        _lib.check(_lib.load().nf4s_gemm_dgrad_sum_ws(
+            dps, descs, ns, len(ws), m, k, out.data_ptr(), workspace.data_ptr(),
+            workspace.numel() * workspace.element_size(), _stream_ptr(out)))
+    else:
+        _lib.check(_lib.load().nf4s_gemm_dgrad_sum(dps, descs, ns, len(ws), m, k,
+                                                   out.data_ptr(), _stream_ptr(out)))
     return out
 
 

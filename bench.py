@@ -36,6 +36,8 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
                        [--gemm-shape NAME [--gemm-mode fwd|dgrad|wgrad|swiglu]]
   --workload quantize runs config 1 alone (oracle quantize on one core, then the
   device quantize of the same matrix) and prints only its line (profiling).
+  --crossover times the 70B layer's forward and input-gradient passes fused and
+  unfused at 256-8192 tokens and prints only that line.
   --gemm-shape times one fused GEMM (70b_q, 70b_k, 70b_gate, 70b_down, 7b_gate,
   7b_down) `steps` times after `warmup` and prints only its line (profiling);
   --gemm-mode bf16-reference times torch.matmul in bf16 on that shape instead.
@@ -89,6 +91,9 @@ def parse():
                     help="approximate CPU time budget of the dequant cpu_baseline sample")
     ap.add_argument("--workload", choices=["all", "dequant", "gemm", "stream", "quantize"],
                     default="all")
+    ap.add_argument("--crossover", action="store_true",
+                    help="time the 70B layer's fused and unfused passes over token counts "
+                         "(256-8192) and print only that line")
     ap.add_argument("--stream-layers", type=int, default=80,
                     help="config 5: number of 70B layers held in pinned host memory")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -657,6 +662,72 @@ def bench_one_gemm(torch, nf4, gemm, args):
                       "k": k, "ms": round(ms, 4), "tflops": round(tf, 1)}), flush=True)
 
 
+def bench_crossover(torch, nf4, gemm, args):
+    """The 70B layer's forward and input-gradient passes, fused against
+    unfused (dequantize the 7 weights to bf16 in one launch, then torch bf16
+    GEMMs, as unfused_measured), over token counts: where the fused kernels'
+    saving (no bf16 copy of the weights written and read) outweighs their
+    lower MFMA rate.  Prints one JSON line."""
+    ws = make_weights(torch, nf4, LAYER_70B, seed=4)
+    wbf = [torch.empty(w.shape, dtype=torch.bfloat16, device="cuda") for w in ws]
+    g = torch.Generator(device="cuda").manual_seed(41)
+    fl_w = sum(2.0 * w.shape[0] * w.shape[1] for w in ws)
+    rows = []
+    for M in (256, 512, 1024, 2048, 4096, 8192):
+        h = torch.randn(M, 8192, device="cuda", generator=g).to(torch.bfloat16)
+        hid = torch.randn(M, 28672, device="cuda", generator=g).to(torch.bfloat16)
+        ins = [h, h, h, h, h, h, hid]
+        ys = [torch.empty(M, w.shape[0], dtype=torch.bfloat16, device="cuda") for w in ws]
+        dys = [torch.randn(M, w.shape[0], device="cuda", generator=g).to(torch.bfloat16)
+               for w in ws]
+        dxs = [torch.empty(M, w.shape[1], dtype=torch.bfloat16, device="cuda") for w in ws]
+
+        def fused_fwd():
+            gemm.linear_fwd_grouped(h, ws[0:3], ys[0:3])
+            gemm.linear_fwd(h, ws[3], ys[3])
+            gemm.linear_fwd_grouped(h, ws[4:6], ys[4:6])
+            gemm.linear_fwd(hid, ws[6], ys[6])
+
+        def fused_dgrad():
+            gemm.linear_dgrad_sum(dys[0:3], ws[0:3], dxs[0])
+            gemm.linear_dgrad(dys[3], ws[3], dxs[3])
+            gemm.linear_dgrad_sum(dys[4:6], ws[4:6], dxs[4])
+            gemm.linear_dgrad(dys[6], ws[6], dxs[6])
+
+        def unfused_fwd():
+            nf4.dequant_batch(ws, wbf)
+            for a, wb, y in zip(ins, wbf, ys):
+                torch.matmul(a, wb.t(), out=y)
+
+        def unfused_dgrad():
+            nf4.dequant_batch(ws, wbf)
+            torch.matmul(dys[0], wbf[0], out=dxs[0])
+            dxs[0].addmm_(dys[1], wbf[1])
+            dxs[0].addmm_(dys[2], wbf[2])
+            torch.matmul(dys[3], wbf[3], out=dxs[3])
+            torch.matmul(dys[4], wbf[4], out=dxs[4])
+            dxs[4].addmm_(dys[5], wbf[5])
+            torch.matmul(dys[6], wbf[6], out=dxs[6])
+
+        k = max(3, args.steps // 5)
+        t = {name: timed(torch, fn, k, 1, warm_s=0.2, name=f"crossover_{name}_m{M}")
+             for name, fn in (("fused_fwd", fused_fwd), ("unfused_fwd", unfused_fwd),
+                              ("fused_dgrad", fused_dgrad), ("unfused_dgrad", unfused_dgrad))}
+        fl = M * fl_w
+        rows.append({"tokens": M,
+                     **{f"{n}_ms": round(v, 4) for n, v in t.items()},
+                     **{f"{n}_tflops": round(fl / (v * 1e-3) / 1e12, 1) for n, v in t.items()},
+                     "fwd_unfused_over_fused_time": round(t["unfused_fwd"] / t["fused_fwd"], 3),
+                     "dgrad_unfused_over_fused_time": round(t["unfused_dgrad"] / t["fused_dgrad"],
+                                                            3)})
+        log(f"crossover M={M}: {rows[-1]}")
+        del h, hid, ins, ys, dys, dxs
+    print(json.dumps({"crossover_70b_layer": rows,
+                      "note": "per pass; unfused = one nf4s_dequant_batch_bf16 of the layer's 7 "
+                              "weights + torch bf16 GEMMs (hipBLASLt); >1 means fused is faster"}),
+          flush=True)
+
+
 def bf16_gemm_reference(torch, dequant_gbs, layer_ms):
     """A plain bf16 GEMM (torch.matmul -> hipBLASLt) of the 70B gate shape, and
     the config-4 rate of an unfused path: dequantize each pass's weights to
@@ -712,6 +783,9 @@ def main():
     from aethelstream_amd import gemm, nf4
     if args.gemm_shape:
         bench_one_gemm(torch, nf4, gemm, args)
+        return
+    if args.crossover:
+        bench_crossover(torch, nf4, gemm, args)
         return
     if args.workload == "quantize":
         # Config 1 alone (the program the quantize kernel trace runs): the

@@ -203,6 +203,32 @@ int32_t nf4s_gemm_dgrad_sum(const uint16_t *const *dys, const nf4s_tensor *ws,
                             int64_t k, uint16_t *dx, void *stream);
 
 /*
+ * nf4s_gemm_dgrad_sum with a workspace for a split-K last round.  When the
+ * output tiles (512 rows x 128 columns of dx) leave a last round of r tiles
+ * on fewer than half the compute units (few tokens: 256 tokens of a 70B
+ * layer give 64 tiles), each of those tiles runs as S = CUs / r slices of
+ * the weights' concatenated reduction (W_0's rows, then W_1's, ...), whose
+ * fp32 partial tiles go to `workspace` and are summed (in slice order) by a
+ * second kernel on the same stream.  No counterpart in the reference: it
+ * only reorders the fp32 sums of backward.rs:79-85, 117-129, 160-168 and
+ * 284-300.  workspace may be NULL or smaller than
+ * nf4s_gemm_dgrad_workspace_size reports: the call then runs without the
+ * split.  Calls that share a workspace must not overlap (one stream, or
+ * ordered streams).
+ */
+int32_t nf4s_gemm_dgrad_sum_ws(const uint16_t *const *dys, const nf4s_tensor *ws,
+                               const int64_t *ns, int32_t count, int64_t m,
+                               int64_t k, uint16_t *dx, void *workspace,
+                               int64_t workspace_bytes, void *stream);
+
+/*
+ * Workspace bytes nf4s_gemm_dgrad_sum_ws uses for these shapes (0: no
+ * split).  No device access.
+ */
+int32_t nf4s_gemm_dgrad_workspace_size(const int64_t *ns, int32_t count,
+                                       int64_t m, int64_t k, int64_t *bytes);
+
+/*
  * nf4s_gemm_fwd_grouped with a workspace for a split-K last round.  When the
  * output tiles leave a last round of r tiles on fewer than half the compute
  * units, each of those tiles runs as S = CUs / r slices of its reduction,

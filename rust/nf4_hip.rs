@@ -137,6 +137,12 @@ extern "C" {
     pub fn nf4s_gemm_dgrad_sum(dys: *const *const u16, ws: *const Nf4sTensor, ns: *const i64,
                                count: i32, m: i64, k: i64, dx: *mut u16,
                                stream: *mut c_void) -> i32;
+    pub fn nf4s_gemm_dgrad_sum_ws(dys: *const *const u16, ws: *const Nf4sTensor, ns: *const i64,
+                                  count: i32, m: i64, k: i64, dx: *mut u16,
+                                  workspace: *mut c_void, workspace_bytes: i64,
+                                  stream: *mut c_void) -> i32;
+    pub fn nf4s_gemm_dgrad_workspace_size(ns: *const i64, count: i32, m: i64, k: i64,
+                                          bytes: *mut i64) -> i32;
     pub fn nf4s_gemm_fwd_grouped_ws(x: *const u16, ws: *const Nf4sTensor, ns: *const i64,
                                     ys: *const *mut u16, count: i32, m: i64, k: i64,
                                     workspace: *mut c_void, workspace_bytes: i64,

@@ -87,6 +87,25 @@ def test_wgrad_argument_rejection():
 
 
 
+
+def test_dgrad_workspace_size_query():
+    """The split-K input-gradient workspace query allocates nothing and needs
+    no kernel (256 CUs assumed without a GPU, the MI355X's)."""
+    lib = _lib.load()
+    f = lib.nf4s_gemm_dgrad_workspace_size
+    out = ctypes.c_int64(-1)
+    ns = (ctypes.c_int64 * 3)(8192, 1024, 1024)
+    assert f(ns, 3, 256, 8192, None) == _lib.NF4S_ERR_INVALID_ARGUMENT
+    assert f(ns, 0, 256, 8192, ctypes.byref(out)) == _lib.NF4S_ERR_INVALID_ARGUMENT
+    assert f(ns, 5, 256, 8192, ctypes.byref(out)) == _lib.NF4S_ERR_INVALID_ARGUMENT
+    # 70B d_h1 at 256 tokens: 64 tiles -> 4 slices of 256 x 256 fp32 per thread.
+    assert f(ns, 3, 256, 8192, ctypes.byref(out)) == 0 and out.value == 64 * 4 * 256 * 256 * 4
+    # 8192 tokens: 1024 tiles, whole rounds, no split.
+    assert f(ns, 3, 8192, 8192, ctypes.byref(out)) == 0 and out.value == 0
+    # n % 64 != 0 is the GEMM's own error; the query reports no split.
+    bad = (ctypes.c_int64 * 1)(100)
+    assert f(bad, 1, 256, 8192, ctypes.byref(out)) == 0 and out.value == 0
+
 def test_wgrad_grouped_argument_rejection():
     """nf4s_gemm_wgrad_grouped validates every product before any launch."""
     lib = _lib.load()

@@ -125,19 +125,21 @@ def test_dgrad_batched_equals_per_step(m, n, k, dq_group):
     # per-step loads, selected by moving the absmax (or its codes) off the
     # alignment the pair loads need: same products, same reduction order,
     # bit-identical outputs.  dq_group 2: each scale covers exactly a pair.
+    # Unsplit: the two producers' split-K slices are sized to their own step
+    # granularity (4 and 2), which changes the fp32 order of a split sum.
     dq = dq_group > 0
     w32 = oracle.gen_normal(43 + n + k, n * k, 0.02)
     w = nf4.quantize_weight(torch.from_numpy(w32).to(DEV).view(n, k), double_quant=dq,
                             dq_group=dq_group or nf4.DQ_GROUP)
     dy, _ = _act(m, n, 11 + m)
-    dx_batched = gemm.linear_dgrad(dy, w)
+    dx_batched = gemm.linear_dgrad(dy, w, split_k=False)
     if dq:
         w2 = nf4.Nf4Weight(packed=w.packed, absmax=None, shape=w.shape,
                            absmax_q=_misaligned(w.absmax_q, 1), absmax_scale=w.absmax_scale,
                            dq_group=w.dq_group)
     else:
         w2 = nf4.Nf4Weight(packed=w.packed, absmax=_misaligned(w.absmax, 1), shape=w.shape)
-    dx_step = gemm.linear_dgrad(dy, w2)
+    dx_step = gemm.linear_dgrad(dy, w2, split_k=False)
     torch.cuda.synchronize()
     assert torch.equal(dx_batched.view(torch.int16), dx_step.view(torch.int16))
 
@@ -415,6 +417,69 @@ def test_fwd_split_k_twice_in_a_row():
         torch.cuda.synchronize()
         assert float((y.float() - exact).norm() / exact.norm()) <= TOL_SAME
 
+
+
+# Split-K input gradient: few tokens leave a last round of at most half the
+# CUs, whose tiles then run as slices of the weights' concatenated reduction.
+# Cases: the batched producer (4 slices of 4 steps); the per-step producer
+# with a slice that straddles two summed weights (steps 10 + 5, slices of 4);
+# the 70B d_h1 sum at 512 tokens (slices of 40 steps, the last one over the
+# end of Wq and all of Wk and Wv); two row blocks at ragged m.
+DGRAD_SPLIT = [(256, [1024], 1024, True), (300, [640, 320], 512, False),
+               (512, [8192, 1024, 1024], 8192, True), (1000, [2048], 4096, True)]
+
+
+@pytest.mark.parametrize("m,ns,k,dq", DGRAD_SPLIT)
+def test_dgrad_split_k_tail(m, ns, k, dq):
+    print(f"dgrad split-K m={m} ns={ns} k={k} dq={dq}", flush=True)
+    ws = [_weight(n, k, 91 + n + i, dq) for i, n in enumerate(ns)]
+    dys = [_act(m, n, 29 + n + i)[0] for i, n in enumerate(ns)]
+    need = gemm.dgrad_workspace_bytes(ns, m, k)
+    got = gemm.linear_dgrad_sum(dys, ws, split_k=True)
+    ref = gemm.linear_dgrad_sum(dys, ws, split_k=False)
+    exact = sum(d.float() @ nf4.dequant(w).float() for d, w in zip(dys, ws))
+    torch.cuda.synchronize()
+    e_split = float((got.float() - exact).norm() / exact.norm())
+    e_ref = float((ref.float() - exact).norm() / exact.norm())
+    assert e_split <= TOL_SAME and e_ref <= TOL_SAME, (e_split, e_ref)
+    if torch.cuda.get_device_properties(0).multi_processor_count == 256:
+        assert need > 0  # these shapes do split on a 256-CU part
+    if len(ns) == 1:
+        one = gemm.linear_dgrad(dys[0], ws[0])
+        torch.cuda.synchronize()
+        assert torch.equal(one.view(torch.int16), got.view(torch.int16))
+
+
+def test_dgrad_split_k_small_workspace_falls_back():
+    """A workspace too small for the split, handed straight to the C entry
+    point: no split, the unsplit result bit for bit."""
+    m, n, k = 256, 1024, 1024
+    w = _weight(n, k, 73, True)
+    dy, _ = _act(m, n, 31)
+    small = torch.empty(4096, dtype=torch.uint8, device=DEV)
+    dx = torch.empty(m, k, dtype=torch.bfloat16, device=DEV)
+    ns = (ctypes.c_int64 * 1)(n)
+    dps = (ctypes.c_void_p * 1)(dy.data_ptr())
+    descs = (_lib.Nf4sTensor * 1)(w.descriptor())
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    _lib.check(_lib.load().nf4s_gemm_dgrad_sum_ws(dps, descs, ns, 1, m, k, dx.data_ptr(),
+                                                  small.data_ptr(), 4096, stream))
+    r = gemm.linear_dgrad(dy, w, split_k=False)
+    torch.cuda.synchronize()
+    assert torch.equal(dx.view(torch.int16), r.view(torch.int16))
+
+
+def test_dgrad_split_k_twice_in_a_row():
+    """Two split launches on one stream reuse one workspace: the second (a
+    smaller shape) must not see the first's partials."""
+    ws_buf = torch.empty(64 << 20, dtype=torch.uint8, device=DEV)
+    for m, n, k, seed in ((512, 2048, 2048, 83), (256, 1024, 512, 84)):
+        w = _weight(n, k, seed, True)
+        dy, _ = _act(m, n, seed)
+        dx = gemm.linear_dgrad(dy, w, split_k=True, workspace=ws_buf)
+        exact = dy.float() @ nf4.dequant(w).float()
+        torch.cuda.synchronize()
+        assert float((dx.float() - exact).norm() / exact.norm()) <= TOL_SAME
 
 # Seeded random shapes: ragged m, any n for the forward (n % 64 == 0 for the
 # input gradient), k a multiple of 64 (per-step and batched producers), both
