@@ -84,3 +84,30 @@ def test_dequant_every_absmax_every_code(dtype):
         del bits, am, w, got, want, gi, wi, gn, same, same2
     torch.cuda.synchronize()
     assert bad == 0
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_dequant_double_quant_every_code_many_scales(dtype):
+    """Double-quant absmax: block absmax = (float)q * scale, one fp32 multiply
+    (the decode the device kernels apply before the product table), for every
+    8-bit code q times 65536 random finite fp32 scales (a 256-block group per
+    scale, huge scales overflowing to inf included), then all 16 NF4 codes."""
+    print(f"double-quant dequant {dtype}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(12)
+    nscale = 1 << 16
+    sbits = torch.randint(0, 0x7F800000, (nscale,), generator=g, device=DEV, dtype=torch.int64)
+    scale = sbits.to(torch.int32).view(torch.float32)
+    q = torch.arange(256, dtype=torch.uint8, device=DEV).repeat(nscale)
+    nblk = q.numel()
+    one_block = torch.tensor([(2 * i << 4) | (2 * i + 1) for i in range(8)] * 4,
+                             dtype=torch.uint8, device=DEV)            # codes 0..15, 4 times
+    w = nf4.Nf4Weight(packed=one_block.repeat(nblk), absmax=None, shape=[nblk * 64],
+                      block_size=64, absmax_q=q, absmax_scale=scale, dq_group=256)
+    got = nf4.dequant(w, dtype=dtype).view(nblk, 4, 16)
+    codes = torch.from_numpy(oracle.codebook().astype(np.float32)).to(DEV)
+    am = q.float() * scale.repeat_interleave(256)
+    want = (am[:, None] * codes[None, :]).to(dtype)[:, None, :].expand(nblk, 4, 16)
+    same = (got.view(torch.int16) == want.view(torch.int16)) | (torch.isnan(got) & torch.isnan(want))
+    torch.cuda.synchronize()
+    assert int((~same).sum()) == 0
+    assert bool(torch.isinf(am).any()) and bool((am == 0).any())  # overflow and q = 0 exercised
