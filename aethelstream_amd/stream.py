@@ -1,4 +1,4 @@
-"""Streamed NF4 layer stack on one GPU.
+"""Streamed NF4 layer stack on one GPU (benchmark config 5).
 
 Host-side mirror of flowcast's VRAM double buffer
 (flowcast/src/vram_double_buffer.rs:196-301, ready.rs:16-51) over the C ABI:

@@ -1,7 +1,7 @@
 """Benchmark of the NF4 streamed-weight path on one MI355X.
 
 Headline (``value``): NF4 dequant to bf16 of a full Llama-7B-shaped decoder
-layer (q/k/v/o 4096x4096, gate/up 11008x4096, down
+layer (benchmark config 2: q/k/v/o 4096x4096, gate/up 11008x4096, down
 4096x11008; block 64; absmax double-quantized to uint8 in groups of 256 with
 an fp32 scale), one grouped launch per step, inputs resident in HBM.
 ``value`` = algorithmic bytes (packed + uint8 absmax + fp32 scales + bf16 out

@@ -140,7 +140,7 @@ def test_dq_encode_zero_group():
 
 
 def test_config1_4096x4096_bitexact():
-    # fp32 4096x4096 ~ N(0, 0.02), block 64, fp32 absmax.
+    # Benchmark config 1: fp32 4096x4096 ~ N(0, 0.02), block 64, fp32 absmax.
     n = 4096 * 4096
     x = oracle.gen_normal(42, n, 0.02)
     pk_ref, am_ref = oracle.quantize_nf4(x)
@@ -160,7 +160,7 @@ LAYER_7B = [("q", 4096, 4096), ("k", 4096, 4096), ("v", 4096, 4096), ("o", 4096,
 
 
 def test_config2_7b_layer_batch_dequant_dq():
-    # the 7 matrices of a Llama-7B layer, double-quant, one
+    # Benchmark config 2: the 7 matrices of a Llama-7B layer, double-quant, one
     # grouped launch; every output element compared with the oracle.
     g = torch.Generator(device=DEV).manual_seed(2)
     ws = []

@@ -208,7 +208,7 @@ def _layer_check(m, n, k, dq, seed, dgrad=False):
 
 @pytest.mark.parametrize("name,n,k", [("gate/up", 11008, 4096), ("down", 4096, 11008)])
 def test_fwd_7b_shapes(name, n, k):
-    # 4096 tokens x NF4 W^T.
+    # Benchmark config 3: 4096 tokens x NF4 W^T.
     _layer_check(4096, n, k, dq=True, seed=3)
 
 
@@ -216,7 +216,7 @@ def test_fwd_7b_shapes(name, n, k):
                                       ("gate/up", 28672, 8192), ("down", 8192, 28672)])
 @pytest.mark.parametrize("dgrad", [False, True])
 def test_70b_shapes(name, n, k, dgrad):
-    # 8192 tokens, forward and input-gradient.
+    # Benchmark config 4: 8192 tokens, forward and input-gradient.
     _layer_check(8192, n, k, dq=True, seed=4, dgrad=dgrad)
 
 
@@ -270,7 +270,7 @@ def test_dgrad_sum_small_vs_oracle(m, k, ns, dq):
 @pytest.mark.parametrize("name,ns,k", [("d_h1 = dq.Wq + dk.Wk + dv.Wv", [8192, 1024, 1024], 8192),
                                        ("d_h2 = d_gate.Wg + d_up.Wu", [28672, 28672], 8192)])
 def test_dgrad_sum_70b_shapes(name, ns, k):
-    # BASELINE config 4 input gradients as the reference accumulates them.
+    # Benchmark config 4 input gradients as the reference accumulates them.
     m = 8192
     g = torch.Generator(device=DEV).manual_seed(8)
     ws = [nf4.quantize_weight(torch.randn(n, k, device=DEV, generator=g) * 0.02, double_quant=True)
@@ -323,7 +323,7 @@ def test_swiglu_small_vs_oracle(m, ff, k, dq):
 
 
 def test_swiglu_70b_shape():
-    # BASELINE config 4 gate/up at 8192 tokens, double-quant.
+    # Benchmark config 4 gate/up at 8192 tokens, double-quant.
     m, ff, k = 8192, 28672, 8192
     g = torch.Generator(device=DEV).manual_seed(12)
     wg = nf4.quantize_weight(torch.randn(ff, k, device=DEV, generator=g) * 0.02, double_quant=True)

@@ -10,7 +10,7 @@ GOLDEN = np.load(__import__("os").path.join(__import__("os").path.dirname(__file
                                             "golden", "nf4_golden.npz"))
 CASES = sorted({k.split("__")[0] for k in GOLDEN.files})
 
-# shard_engine/src/nf4.rs:6-23 as bits (the survey's table of the literals).
+# shard_engine/src/nf4.rs:6-23 as bits.
 CODE_BITS = [0xbf800000, 0xbf3239b1, 0xbf066b30, 0xbeca32a0, 0xbe91a24d, 0xbe3d353f,
              0xbdba7872, 0x00000000, 0x3da2faff, 0x3e24cae3, 0x3e7c04dd, 0x3ead033a,
              0x3ee1a4b8, 0x3f1007ab, 0x3f3913b3, 0x3f800000]

@@ -174,7 +174,7 @@ LAYER_70B = [("q", 8192, 8192), ("k", 1024, 8192), ("v", 1024, 8192), ("o", 8192
 
 
 def test_config5_80_streamed_70b_layers():
-    """BASELINE config 5 at its workload: 80 double-quantized 70B-shaped
+    """Benchmark config 5 at its workload: 80 double-quantized 70B-shaped
     layers (441 MB blobs) in pinned memory, 4096 tokens, streamed through the
     double buffer while the previous layer's fused forwards run.  The blobs
     alternate between two distinct layers, so a slot read before its copy
