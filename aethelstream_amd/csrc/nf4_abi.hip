@@ -29,7 +29,9 @@ int32_t validate_tensor(const nf4s_tensor *t, int64_t n) {
   if (t->packed_len < 0 || t->absmax_len < 0 || t->scale_len < 0)
     return fail(NF4S_ERR_INVALID_ARGUMENT, "negative buffer length");
   const bool dq = t->absmax_q != nullptr;
-  if (dq == (t->absmax != nullptr))
+  // An empty tensor's buffers may all be NULL (an empty tensor's data
+  // pointer is), so the rule only binds when there are elements.
+  if (n > 0 && dq == (t->absmax != nullptr))
     return fail(NF4S_ERR_INVALID_ARGUMENT, "exactly one of absmax / absmax_q must be set");
   // shard_engine/src/nf4.rs:43-57, same order and wording.
   const int64_t nb = (n + t->block_size - 1) / t->block_size;

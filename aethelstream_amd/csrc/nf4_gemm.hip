@@ -1433,10 +1433,12 @@ static AbsmaxRef absmax_of(const nf4s_tensor &t) {
   return a;
 }
 
-// Shared argument checks of the two GEMM entry points.  W is [wn, wk].
+// Shared argument checks of the two GEMM entry points.  W is [wn, wk].  With
+// m == 0 (no tokens) the activation and output may be NULL, as an empty
+// tensor's data pointer is; the weight is still checked.
 static int32_t check_gemm(const uint16_t *act, const nf4s_tensor *w, int64_t m, int64_t wn,
                           int64_t wk, const uint16_t *out) {
-  if (act == nullptr || out == nullptr)
+  if (m != 0 && (act == nullptr || out == nullptr))
     return fail(NF4S_ERR_INVALID_ARGUMENT, "activation or output is NULL");
   if (m < 0 || wn <= 0 || wk <= 0)
     return fail(NF4S_ERR_INVALID_ARGUMENT, "bad GEMM shape m=%lld n=%lld k=%lld",

@@ -10,7 +10,9 @@
  *   - calls are stream-ordered and asynchronous unless stated otherwise;
  *     they allocate no device memory and let no C++ exception escape;
  *   - calls on different streams may run concurrently; each call reads only
- *     its inputs and writes only its outputs.
+ *     its inputs and writes only its outputs;
+ *   - a call over zero elements or zero tokens does nothing and returns
+ *     NF4S_OK; its data pointers may then be NULL.
  *
  * Paths in citations are relative to the AethelStream source tree.
  */

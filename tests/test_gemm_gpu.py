@@ -584,3 +584,30 @@ def test_fwd_grouped_70b_launches(name, ns, k):
         assert err <= TOL_SAME, (name, err)
         del sep, ref
     torch.cuda.synchronize()
+
+
+def test_zero_tokens_and_empty_tensors():
+    """Zero tokens through every GEMM entry point, and empty tensors through
+    quantize and dequant: empty outputs, no launch errors, and the stream
+    stays usable (a normal call after them is still exact)."""
+    w = _weight(256, 128, 3, dq=True)
+    w2 = _weight(128, 128, 4, dq=True)
+    x0 = torch.zeros(0, 128, dtype=torch.bfloat16, device=DEV)
+    assert gemm.linear_fwd(x0, w).shape == (0, 256)
+    assert gemm.linear_fwd(x0, w, split_k=False).shape == (0, 256)
+    ys = gemm.linear_fwd_grouped(x0, [w, w2])
+    assert [tuple(y.shape) for y in ys] == [(0, 256), (0, 128)]
+    dy0 = torch.zeros(0, 256, dtype=torch.bfloat16, device=DEV)
+    assert gemm.linear_dgrad(dy0, w).shape == (0, 128)
+    dx = gemm.linear_dgrad_sum([dy0, torch.zeros(0, 128, dtype=torch.bfloat16, device=DEV)],
+                               [w, w2])
+    assert dx.shape == (0, 128)
+    assert gemm.linear_swiglu(x0, w, _weight(256, 128, 5, dq=True)).shape == (0, 256)
+    r = nf4.quantize_nf4(torch.zeros(0, dtype=torch.float32, device=DEV))
+    assert r.packed.numel() == 0 and r.absmax.numel() == 0
+    assert nf4.dequant(nf4.Nf4Weight(packed=r.packed, absmax=r.absmax, shape=[0])).numel() == 0
+    x, xh = _act(64, 128, 6)
+    y = gemm.linear_fwd(x, w)
+    torch.cuda.synchronize()
+    ref = xh.astype(np.float64) @ _deq_host(w, f16=False).astype(np.float64).T
+    assert rel_l2(y.float().cpu().numpy(), ref) <= TOL_SAME
