@@ -1434,8 +1434,9 @@ static AbsmaxRef absmax_of(const nf4s_tensor &t) {
 }
 
 // Shared argument checks of the two GEMM entry points.  W is [wn, wk].  With
-// m == 0 (no tokens) the activation and output may be NULL, as an empty
-// tensor's data pointer is; the weight is still checked.
+// m == 0 (no tokens) nothing is read or written: the activation and output
+// pointers may be NULL or unaligned (an empty tensor's or vector's data
+// pointer), and only the weight's shape is checked.
 static int32_t check_gemm(const uint16_t *act, const nf4s_tensor *w, int64_t m, int64_t wn,
                           int64_t wk, const uint16_t *out) {
   if (m != 0 && (act == nullptr || out == nullptr))
@@ -1451,6 +1452,7 @@ static int32_t check_gemm(const uint16_t *act, const nf4s_tensor *w, int64_t m, 
   if (wk % 64 != 0)
     return fail(NF4S_ERR_UNSUPPORTED_SHAPE, "fused GEMM needs k %% 64 == 0, got %lld",
                 (long long)wk);
+  if (m == 0) return NF4S_OK;
   if (!aligned(act, 16) || !aligned(w->packed, 16))
     return fail(NF4S_ERR_MISALIGNED, "activation and packed weights must be 16-byte aligned");
   if (!aligned(out, 2)) return fail(NF4S_ERR_MISALIGNED, "output must be 2-byte aligned");

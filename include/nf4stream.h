@@ -11,8 +11,10 @@
  *     they allocate no device memory and let no C++ exception escape;
  *   - calls on different streams may run concurrently; each call reads only
  *     its inputs and writes only its outputs;
- *   - a call over zero elements or zero tokens does nothing and returns
- *     NF4S_OK; its data pointers may then be NULL.
+ *   - a call over zero elements or zero tokens reads no input and returns
+ *     NF4S_OK; its empty buffers may then be NULL or unaligned (the weight
+ *     gradient over zero tokens still sets dW to 0, or leaves it when
+ *     accumulating).
  *
  * Paths in citations are relative to the AethelStream source tree.
  */
