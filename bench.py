@@ -752,6 +752,21 @@ def bf16_gemm_reference(torch, dequant_gbs, layer_ms):
     return res
 
 
+def hbm_copy_ceiling(torch):
+    """The box's measured HBM ceiling for a plain streaming copy: torch's
+    device copy of 1 GiB (1 GiB read + 1 GiB written per call), far larger
+    than the 256 MB Infinity Cache.  A reported ceiling beside the 8 TB/s
+    nominal peak that `roofline.frac` is quoted against."""
+    n = 1 << 30
+    a = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+    b = torch.empty_like(a)
+    ms = timed(torch, lambda: b.copy_(a), 10, 2, name="hbm_copy")
+    gbs = 2.0 * n / (ms * 1e-3) / 1e9
+    del a, b
+    return {"op": "torch copy, 1 GiB each way", "gbs": round(gbs, 1),
+            "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4)}
+
+
 def copy_calibration(torch):
     """A plain device copy of exactly 1 GiB read + 1 GiB written (the known
     byte count that rocprofv3's FETCH_SIZE / WRITE_SIZE are scaled against)."""
@@ -823,6 +838,8 @@ def main():
         line["roofline"] = {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
                             "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
                             "traffic": read_traffic()}
+        log("HBM copy ceiling")
+        line["hbm_copy_ceiling"] = hbm_copy_ceiling(torch)
         log("PCIe-inclusive host-slice dequant")
         line["dequant_host_roundtrip"] = bench_dequant_host(torch, nf4, args)
     if args.workload in ("all", "gemm"):
