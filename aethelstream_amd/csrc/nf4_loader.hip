@@ -510,7 +510,8 @@ int32_t nf4s_loader_param_info(nf4s_loader *L, const char *name, nf4s_param_info
   int64_t numel = 1;
   for (int i = 0; i < out->ndim; ++i) {
     out->shape[i] = t->shape[i];
-    numel *= t->shape[i];
+    if (__builtin_mul_overflow(numel, t->shape[i], &numel))
+      return malformed(name, "shape element count overflows 64 bits");
   }
   out->numel = numel;
   out->byte_length = t->byte_length;
@@ -522,6 +523,8 @@ int32_t nf4s_loader_param_info(nf4s_loader *L, const char *name, nf4s_param_info
     out->absmax_len = t->dq ? t->q_length : t->absmax_length / 4;
     out->scale_len = t->dq ? t->scale_length / 4 : 0;
     out->dq_group = t->dq ? (int32_t)t->dq_group : 0;
+    if (t->byte_length > INT64_MAX / 2)
+      return malformed(name, "byte_length %lld too large", (long long)t->byte_length);
     out->out_elems = 2 * t->byte_length;  // nf4.rs:103
   } else {
     out->precision = 0;
@@ -549,15 +552,23 @@ int32_t nf4s_loader_load_layer(nf4s_loader *L, uint32_t layer, const uint8_t **d
 }
 
 // Device staging bytes nf4s_loader_load_param_f16 needs for `name` (0 for an
-// fp16 entry, which is copied straight into the output).
+// fp16 entry, which is copied straight into the output).  An NF4 entry is
+// checked against its shard file first, as the load does, so its lengths are
+// bounded by the file size before they are summed.
 int32_t nf4s_loader_staging_size(nf4s_loader *L, const char *name, int64_t *bytes) {
   clear_error();
   if (L == nullptr || bytes == nullptr) return fail(NF4S_ERR_INVALID_ARGUMENT, "bad args");
   *bytes = 0;
   const TensorInfo *t;
-  const int32_t rc = lookup(L, name, &t);
+  int32_t rc = lookup(L, name, &t);
   if (rc != NF4S_OK) return rc;
-  if (is_nf4(*t)) *bytes = staging_of(*t).bytes;
+  if (!is_nf4(*t)) return NF4S_OK;
+  const MappedFile *m;
+  rc = get_mmap(L, t->file_path, &m);
+  if (rc != NF4S_OK) return rc;
+  rc = check_nf4(name, *t, *m);
+  if (rc != NF4S_OK) return rc;
+  *bytes = staging_of(*t).bytes;
   return NF4S_OK;
 }
 
@@ -583,7 +594,7 @@ int32_t nf4s_loader_load_param_f16(nf4s_loader *L, const char *name, uint16_t *o
       return malformed(name, "tensor data out of bounds: offset %lld + length %lld > mmap %llu",
                        (long long)t->byte_offset, (long long)t->byte_length,
                        (unsigned long long)m->size);
-    if (out_len < 0 || out_len * 2 < t->byte_length)
+    if (out_len < 0 || out_len < t->byte_length / 2 + t->byte_length % 2)
       return fail(NF4S_ERR_INVALID_ARGUMENT, "output holds %lld elements, need %lld",
                   (long long)out_len, (long long)(t->byte_length / 2));
     const hipError_t e = hipMemcpyAsync(out, m->data + t->byte_offset, (size_t)t->byte_length,

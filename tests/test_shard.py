@@ -257,3 +257,39 @@ def test_pack_layer_blob_bytes_and_descriptors(tmp_path, double_quant):
         L.pack_layer(names, base, 256)
     with pytest.raises(shard.MalformedIndexEntry, match="not nf4"):
         L.pack_layer(["model.layers.0.norm"])
+
+
+@pytest.mark.parametrize("update,what", [
+    ({"shape": [1 << 40, 1 << 40]}, "shape element count overflows 64 bits"),
+    ({"byte_length": (1 << 63) - 1}, "byte_length"),
+])
+def test_param_info_sizes_do_not_overflow(shard_dir, update, what):
+    # Products and doublings of index sizes are checked, not wrapped (found
+    # by fuzzing the loader's host code under UBSan).
+    d, index, registry, _ = shard_dir
+    e = dict(index["model.layers.0.q"])
+    e.update(update)
+    index = dict(index)
+    index["model.layers.0.q"] = e
+    write_index(d, index, registry)
+    L = shard.ShardLoader(d)
+    info = _lib.Nf4sParamInfo()
+    rc = _lib.load().nf4s_loader_param_info(L._h, b"model.layers.0.q", ctypes.byref(info))
+    assert rc == _lib.NF4S_ERR_MALFORMED_INDEX
+    assert what in _lib.load().nf4s_last_error_message().decode()
+
+
+def test_staging_size_checks_the_entry_first(shard_dir):
+    # Lengths near 2^63 used to be rounded and summed unchecked; the size
+    # query now rejects an entry out of bounds of its file, as the load does.
+    d, index, registry, _ = shard_dir
+    e = dict(index["model.layers.0.q"])
+    e.update(nf4_absmax_length=(1 << 63) - 1)
+    index = dict(index)
+    index["model.layers.0.q"] = e
+    write_index(d, index, registry)
+    L = shard.ShardLoader(d)
+    n = ctypes.c_int64(7)
+    rc = _lib.load().nf4s_loader_staging_size(L._h, b"model.layers.0.q", ctypes.byref(n))
+    assert rc == _lib.NF4S_ERR_MALFORMED_INDEX and n.value == 0
+    assert "absmax data out of bounds" in _lib.load().nf4s_last_error_message().decode()
