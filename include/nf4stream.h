@@ -417,7 +417,8 @@ int32_t nf4s_loader_load_layer(nf4s_loader *l, uint32_t layer, const uint8_t **d
 
 /* Device staging bytes nf4s_loader_load_param_f16 needs for `name`: the
  * packed bytes, absmax part and scales at 256-byte boundaries (0 for an fp16
- * entry).  Allocates nothing. */
+ * entry).  An NF4 entry is first checked against its shard file, with the
+ * errors nf4s_loader_load_param_f16 reports.  Allocates nothing. */
 int32_t nf4s_loader_staging_size(nf4s_loader *l, const char *name, int64_t *bytes);
 
 /* ShardLoader::load_param (loader.rs:78-206) into a device f16 buffer of
