@@ -373,6 +373,9 @@ static int32_t wgrad_grouped(const uint16_t *const *dys, const int64_t *ns, floa
   if (m < 0 || k <= 0)
     return fail(NF4S_ERR_INVALID_ARGUMENT, "bad weight-gradient shape m=%lld k=%lld",
                 (long long)m, (long long)k);
+  constexpr int64_t kMaxDim = (int64_t)1 << 39;  // tile counts below are 32-bit
+  if (k > kMaxDim)
+    return fail(NF4S_ERR_UNSUPPORTED_SHAPE, "weight-gradient k=%lld beyond 2^39", (long long)k);
   if (k % 8 != 0)
     return fail(NF4S_ERR_UNSUPPORTED_SHAPE, "weight gradient needs k %% 8 == 0, got k=%lld",
                 (long long)k);
@@ -381,9 +384,11 @@ static int32_t wgrad_grouped(const uint16_t *const *dys, const int64_t *ns, floa
   // Lane offsets are 32-bit and must stay below 2^31 for every row a step
   // addresses, including the rows past m of the last 32-token step (which
   // read as zero only while their offsets do not wrap onto real rows).
+  // The comparisons divide instead of multiplying, so no caller size can
+  // overflow them.
   const int64_t lim = ((int64_t)1 << 31) - 1;
-  const int64_t rows = (m + kWgStep - 1) / kWgStep * kWgStep;
-  if (rows * k * 2 > lim)
+  const int64_t rows = m / kWgStep * kWgStep + (m % kWgStep ? kWgStep : 0);
+  if (rows > 0 && k > lim / 2 / rows)
     return fail(NF4S_ERR_UNSUPPORTED_SHAPE,
                 "x larger than 2 GiB with m rounded up to 32 (m=%lld k=%lld)", (long long)m,
                 (long long)k);
@@ -402,13 +407,19 @@ static int32_t wgrad_grouped(const uint16_t *const *dys, const int64_t *ns, floa
     if (n <= 0)
       return fail(NF4S_ERR_INVALID_ARGUMENT, "bad weight-gradient shape m=%lld n=%lld k=%lld",
                   (long long)m, (long long)n, (long long)k);
+    if (n > kMaxDim)
+      return fail(NF4S_ERR_UNSUPPORTED_SHAPE, "weight-gradient n=%lld beyond 2^39", (long long)n);
     if (n % 8 != 0)
       return fail(NF4S_ERR_UNSUPPORTED_SHAPE, "weight gradient needs n %% 8 == 0 and k %% 8 == 0, "
                   "got n=%lld k=%lld", (long long)n, (long long)k);
     if (m > 0 && !aligned(dys[i], 16))
       return fail(NF4S_ERR_MISALIGNED, "dy and x must be 16-byte aligned");
     if (!aligned(dws[i], 4)) return fail(NF4S_ERR_MISALIGNED, "dw must be 4-byte aligned");
-    if (rows * n * 2 > lim)
+    int64_t nk;
+    if (__builtin_mul_overflow(n, k, &nk))
+      return fail(NF4S_ERR_UNSUPPORTED_SHAPE, "dW of %lld x %lld elements overflows 64 bits",
+                  (long long)n, (long long)k);
+    if (rows > 0 && n > lim / 2 / rows)
       return fail(NF4S_ERR_UNSUPPORTED_SHAPE,
                   "dy or x larger than 2 GiB with m rounded up to 32 (m=%lld n=%lld k=%lld)",
                   (long long)m, (long long)n, (long long)k);

@@ -1444,7 +1444,17 @@ static int32_t check_gemm(const uint16_t *act, const nf4s_tensor *w, int64_t m, 
   if (m < 0 || wn <= 0 || wk <= 0)
     return fail(NF4S_ERR_INVALID_ARGUMENT, "bad GEMM shape m=%lld n=%lld k=%lld",
                 (long long)m, (long long)wn, (long long)wk);
-  const int32_t rc = validate_tensor(w, wn * wk);
+  // Tile counts are 32-bit: (dim + 511) / 512 must fit before the launch
+  // code bounds the tile total.
+  constexpr int64_t kMaxDim = (int64_t)1 << 39;
+  if (m > kMaxDim || wn > kMaxDim || wk > kMaxDim)
+    return fail(NF4S_ERR_UNSUPPORTED_SHAPE, "GEMM dimension beyond 2^39: m=%lld n=%lld k=%lld",
+                (long long)m, (long long)wn, (long long)wk);
+  int64_t numel;
+  if (__builtin_mul_overflow(wn, wk, &numel))
+    return fail(NF4S_ERR_UNSUPPORTED_SHAPE, "weight of %lld x %lld elements overflows 64 bits",
+                (long long)wn, (long long)wk);
+  const int32_t rc = validate_tensor(w, numel);
   if (rc != NF4S_OK) return rc;
   if (w->block_size != 64)
     return fail(NF4S_ERR_UNSUPPORTED_SHAPE, "fused GEMM needs block_size 64, got %d",
@@ -1589,9 +1599,10 @@ static int32_t launch_dgrad(GroupedArgs &ga, int64_t nsteps, hipStream_t s, void
 // Workspace bytes the split-K input gradient over these weights needs (0: no
 // split), for either producer's step granularity.
 static int64_t dgrad_workspace_bytes(const int64_t *ns, int32_t count, int64_t m, int64_t k) {
-  if (m <= 0 || k <= 0 || k % 64 != 0) return 0;
+  constexpr int64_t kMaxDim = (int64_t)1 << 39;  // beyond it the GEMM rejects the shape
+  if (m <= 0 || m > kMaxDim || k <= 0 || k > kMaxDim || k % 64 != 0) return 0;
   for (int32_t i = 0; i < count; ++i)
-    if (ns[i] <= 0 || ns[i] % 64 != 0) return 0;
+    if (ns[i] <= 0 || ns[i] > kMaxDim || ns[i] % 64 != 0) return 0;
   const int64_t T = ((m + kTileM - 1) / kTileM) * ((k + kTileO - 1) / kTileO);
   const int64_t steps = dgrad_steps(ns, count);
   int64_t best = 0;
@@ -1769,9 +1780,10 @@ static int32_t gemm_dgrad_groups(const uint16_t *const *dys, const nf4s_tensor *
 // kind, so this is the largest plan over every subset of the weights and
 // both producers' step multiples: enough for any partition into launches.
 static int64_t fwd_workspace_bytes(const int64_t *ns, int32_t count, int64_t m, int64_t k) {
-  if (m <= 0 || k <= 0 || k % 64 != 0) return 0;
+  constexpr int64_t kMaxDim = (int64_t)1 << 39;  // beyond it the GEMM rejects the shape
+  if (m <= 0 || m > kMaxDim || k <= 0 || k > kMaxDim || k % 64 != 0) return 0;
   for (int32_t i = 0; i < count; ++i)
-    if (ns[i] <= 0) return 0;
+    if (ns[i] <= 0 || ns[i] > kMaxDim) return 0;
   const int64_t tiles_m = (m + kTileM - 1) / kTileM;
   int64_t best = 0;
   for (uint32_t set = 1; set < (1u << count); ++set) {

@@ -184,3 +184,29 @@ def test_wgrad_rejects_offsets_past_2gib_in_the_last_step():
     rc = lib.nf4s_gemm_wgrad(0x1000, 0x2000, 1, 1 << 25, 8, 0x3000, 0, None)
     assert rc == _lib.NF4S_ERR_UNSUPPORTED_SHAPE
     assert b"m rounded up to 32" in lib.nf4s_last_error_message()
+
+
+def test_huge_sizes_are_rejected_not_wrapped():
+    """Caller sizes whose products or tile counts would overflow are refused
+    before any device work (checked division instead of wrapping products)."""
+    lib = _lib.load()
+    d = _desc(packed_len=1 << 62, absmax_len=1 << 56, bs=64)
+    x, out = 0x1000, 0x2000
+    f = lib.nf4s_gemm_fwd
+    assert f(x, ctypes.byref(d), 64, 1 << 40, 64, out, None) == _lib.NF4S_ERR_UNSUPPORTED_SHAPE
+    assert b"beyond 2^39" in lib.nf4s_last_error_message()
+    assert f(x, ctypes.byref(d), 1 << 62, 64, 64, out, None) == _lib.NF4S_ERR_UNSUPPORTED_SHAPE
+    assert lib.nf4s_gemm_dgrad(x, ctypes.byref(d), 64, 1 << 35, 1 << 35, out, None) == \
+        _lib.NF4S_ERR_UNSUPPORTED_SHAPE
+    assert b"overflows 64 bits" in lib.nf4s_last_error_message()
+    w = lib.nf4s_gemm_wgrad
+    assert w(x, x, 1 << 62, 64, 8, out, 0, None) == _lib.NF4S_ERR_UNSUPPORTED_SHAPE
+    assert w(x, x, 64, 64, 1 << 45, out, 0, None) == _lib.NF4S_ERR_UNSUPPORTED_SHAPE
+    assert w(x, x, 0, 1 << 38, 1 << 38, out, 0, None) == _lib.NF4S_ERR_UNSUPPORTED_SHAPE
+    assert b"overflows 64 bits" in lib.nf4s_last_error_message()
+    size = ctypes.c_int64(-1)
+    ns = (ctypes.c_int64 * 1)(1 << 45)
+    assert lib.nf4s_gemm_dgrad_workspace_size(ns, 1, 256, 8192, ctypes.byref(size)) == 0
+    assert size.value == 0
+    assert lib.nf4s_gemm_fwd_workspace_size(ns, 1, 1 << 62, 8192, ctypes.byref(size)) == 0
+    assert size.value == 0
