@@ -29,6 +29,10 @@ inline bool aligned(const void *p, uintptr_t a) {
   return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0;
 }
 
+// ceil(a / b) for a >= 0, b > 0, without the a + b - 1 that wraps for
+// caller sizes near 2^63.
+inline int64_t ceil_div(int64_t a, int64_t b) { return a / b + (a % b != 0 ? 1 : 0); }
+
 // log2 of a power-of-two double-quant group (validate_tensor checks it).
 inline int32_t group_shift(int32_t group) {
   int32_t s = 0;

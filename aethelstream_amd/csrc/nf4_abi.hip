@@ -34,11 +34,11 @@ int32_t validate_tensor(const nf4s_tensor *t, int64_t n) {
   if (n > 0 && dq == (t->absmax != nullptr))
     return fail(NF4S_ERR_INVALID_ARGUMENT, "exactly one of absmax / absmax_q must be set");
   // shard_engine/src/nf4.rs:43-57, same order and wording.
-  const int64_t nb = (n + t->block_size - 1) / t->block_size;
+  const int64_t nb = ceil_div(n, t->block_size);
   if (t->absmax_len < nb)
     return fail(NF4S_ERR_ABSMAX_TOO_SMALL, "absmax too small: %lld < %lld",
                 (long long)t->absmax_len, (long long)nb);
-  if (t->packed_len * 2 < n)
+  if (t->packed_len < ceil_div(n, 2))
     return fail(NF4S_ERR_PACKED_TOO_SMALL, "packed too small: %lld < %lld",
                 (long long)(t->packed_len * 2), (long long)n);
   if (n > 0 && t->packed == nullptr)
@@ -47,7 +47,7 @@ int32_t validate_tensor(const nf4s_tensor *t, int64_t n) {
     if (t->dq_group <= 0 || (t->dq_group & (t->dq_group - 1)) != 0)
       return fail(NF4S_ERR_INVALID_ARGUMENT, "dq_group must be a power of two, got %d",
                   t->dq_group);
-    const int64_t ng = (nb + t->dq_group - 1) / t->dq_group;
+    const int64_t ng = ceil_div(nb, t->dq_group);
     if (t->scale_len < ng || (ng > 0 && t->absmax_scale == nullptr))
       return fail(NF4S_ERR_ABSMAX_TOO_SMALL, "absmax scale too small: %lld < %lld",
                   (long long)t->scale_len, (long long)ng);

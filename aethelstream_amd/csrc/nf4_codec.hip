@@ -638,7 +638,7 @@ static bool quantize_vec_ok(const T *x, const uint8_t *packed) {
 
 template <typename T>
 static int32_t quantize64(const T *x, int64_t n, uint8_t *packed, float *absmax, hipStream_t s) {
-  const int64_t ntiles = (n + 511) / 512;
+  const int64_t ntiles = ceil_div(n, 512);
   int64_t grid = ((ntiles + kQuantU - 1) / kQuantU + 3) / 4;
   if (grid > kQuantMaxGrid) grid = kQuantMaxGrid;
   if (quantize_vec_ok(x, packed))
@@ -663,8 +663,8 @@ static int32_t quantize_dq(const T *x, int64_t n, int32_t block_size, int32_t gr
   if (n == 0) return NF4S_OK;
   if (x == nullptr || packed == nullptr || q == nullptr || scale == nullptr)
     return fail(NF4S_ERR_INVALID_ARGUMENT, "NULL buffer");
-  const int64_t nb = (n + 63) / 64;
-  const int64_t ng = (nb + group - 1) / group;
+  const int64_t nb = ceil_div(n, 64);
+  const int64_t ng = ceil_div(nb, group);
   if (ng > 0x7fffffff) return fail(NF4S_ERR_UNSUPPORTED_SHAPE, "too many groups");
   const size_t lds = (size_t)group * sizeof(float);
   const uint32_t grid = (uint32_t)(ng < kQuantMaxGrid ? ng : kQuantMaxGrid);
@@ -691,14 +691,14 @@ int32_t nf4s_quantize(const float *x, int64_t n, int32_t block_size, uint8_t *pa
   if (n == 0) return NF4S_OK;
   if (x == nullptr || packed == nullptr || absmax == nullptr)
     return fail(NF4S_ERR_INVALID_ARGUMENT, "NULL buffer");
-  const int64_t nb = (n + block_size - 1) / block_size;
+  const int64_t nb = ceil_div(n, block_size);
   hipStream_t s = as_stream(stream);
   if (block_size == 64) return quantize64<float>(x, n, packed, absmax, s);
   hipLaunchKernelGGL(absmax_generic_kernel, dim3(grid_for(nb, 256)), dim3(256), 0, s, x, n,
                      block_size, absmax, nb);
   int32_t rc = check_launch("absmax_generic_kernel");
   if (rc != NF4S_OK) return rc;
-  const int64_t npk = (n + 1) / 2;
+  const int64_t npk = ceil_div(n, 2);
   hipLaunchKernelGGL(codes_generic_kernel, dim3(grid_for(npk, 256)), dim3(256), 0, s, x, n,
                      block_size, absmax, packed, npk);
   return check_launch("codes_generic_kernel");
@@ -738,7 +738,7 @@ int32_t nf4s_dq_encode(const float *absmax, int64_t nblocks, int32_t group, uint
   if (nblocks == 0) return NF4S_OK;
   if (absmax == nullptr || q == nullptr || scale == nullptr)
     return fail(NF4S_ERR_INVALID_ARGUMENT, "NULL buffer");
-  const int64_t ng = (nblocks + group - 1) / group;
+  const int64_t ng = ceil_div(nblocks, group);
   if (ng > 0x7fffffff) return fail(NF4S_ERR_UNSUPPORTED_SHAPE, "too many groups");
   hipLaunchKernelGGL(dq_encode_kernel, dim3((uint32_t)ng), dim3(256), 0, as_stream(stream),
                      absmax, nblocks, group, q, scale);

@@ -204,6 +204,14 @@ def test_huge_sizes_are_rejected_not_wrapped():
     assert w(x, x, 64, 64, 1 << 45, out, 0, None) == _lib.NF4S_ERR_UNSUPPORTED_SHAPE
     assert w(x, x, 0, 1 << 38, 1 << 38, out, 0, None) == _lib.NF4S_ERR_UNSUPPORTED_SHAPE
     assert b"overflows 64 bits" in lib.nf4s_last_error_message()
+    # Descriptor checks at element counts near 2^63 (ceil divisions, not sums).
+    big = (1 << 63) - 1
+    d = _desc(packed_len=1 << 62, absmax_len=1 << 56, bs=64)
+    assert lib.nf4s_dequant_bf16(ctypes.byref(d), big, out, None) == \
+        _lib.NF4S_ERR_ABSMAX_TOO_SMALL
+    d = _desc(packed_len=(1 << 62) - 1, absmax_len=1 << 62, bs=64)
+    assert lib.nf4s_dequant_bf16(ctypes.byref(d), big, out, None) == \
+        _lib.NF4S_ERR_PACKED_TOO_SMALL
     size = ctypes.c_int64(-1)
     ns = (ctypes.c_int64 * 1)(1 << 45)
     assert lib.nf4s_gemm_dgrad_workspace_size(ns, 1, 256, 8192, ctypes.byref(size)) == 0
