@@ -152,7 +152,10 @@ int32_t nf4s_dequant_batch_bf16(const nf4s_tensor *ts, const int64_t *ns,
  * Replaces matmul_tb (doublepass/src/math.rs:9-21) at its call sites in
  * single_layer_forward (doublepass/src/forward.rs:174-176,244,251-252,255) and
  * the recompute forward (doublepass/src/backward.rs:447-451).
- * Requires k % 64 == 0, block_size == 64, x/y 16-byte aligned.
+ * Requires k % 64 == 0, block_size == 64, x/y 16-byte aligned.  Every GEMM
+ * entry point takes m, n and k up to 2^39 (tile counts are 32-bit; the launch
+ * also bounds the total of output tiles by 2^31 - 1) and rejects larger ones
+ * with NF4S_ERR_UNSUPPORTED_SHAPE.
  */
 int32_t nf4s_gemm_fwd(const uint16_t *x, const nf4s_tensor *w, int64_t m,
                       int64_t n, int64_t k, uint16_t *y, void *stream);
