@@ -34,7 +34,13 @@ def rms_norm_fwd(x: torch.Tensor, w: torch.Tensor, eps: float = EPS,
         out = torch.empty(m, d, dtype=torch.bfloat16, device=x.device)
     if rms is None:
         rms = torch.empty(m, dtype=torch.float32, device=x.device)
-    if out.dtype != torch.bfloat16 or list(out.shape) != [m, d] or not out.is_contiguous():
+    # A caller's out / rms is written by the kernel: it must be contiguous
+    # device memory on x's device (a host tensor's pointer would reach the
+    # kernel, a strided one would be overwritten as if contiguous).
+    _require_cuda(out, rms)
+    if out.device != x.device or rms.device != x.device:
+        raise ValueError("out and rms must be on x's device")
+    if out.dtype != torch.bfloat16 or list(out.shape) != [m, d]:
         raise ValueError("out must be a contiguous bfloat16 [M, d] tensor")
     if rms.dtype != torch.float32 or rms.numel() < m:
         raise ValueError("rms must hold M float32 values")

@@ -75,3 +75,25 @@ def test_rmsnorm_rejects_bad_shapes():
     x = torch.zeros(2, 6, device="cuda")
     with pytest.raises(Exception, match="d % 4"):
         norm.rms_norm_fwd(x, torch.ones(6, device="cuda"))
+
+
+def test_rmsnorm_rejects_host_or_strided_outputs():
+    """A caller's out / rms must be contiguous device memory: a host tensor
+    or a strided view raises before any launch (the kernel would write
+    through a host pointer, or over a strided rms as if contiguous)."""
+    x = torch.ones(4, 8, device="cuda")
+    w = torch.ones(8, device="cuda")
+    good_out = torch.empty(4, 8, dtype=torch.bfloat16, device="cuda")
+    good_rms = torch.empty(4, dtype=torch.float32, device="cuda")
+    bad = [
+        dict(out=torch.empty(4, 8, dtype=torch.bfloat16), rms=good_rms),           # host out
+        dict(out=good_out, rms=torch.empty(4, dtype=torch.float32)),               # host rms
+        dict(out=good_out, rms=torch.empty(8, dtype=torch.float32, device="cuda")[::2]),
+        dict(out=torch.empty(8, 8, dtype=torch.bfloat16, device="cuda")[::2], rms=good_rms),
+    ]
+    for kw in bad:
+        with pytest.raises(ValueError):
+            norm.rms_norm_fwd(x, w, **kw)
+    y, r = norm.rms_norm_fwd(x, w, out=good_out, rms=good_rms)
+    torch.cuda.synchronize()
+    assert torch.allclose(r, torch.ones_like(r), atol=1e-5)  # sqrt(1 + eps)
