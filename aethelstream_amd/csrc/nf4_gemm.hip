@@ -26,7 +26,6 @@
 // accumulator layout is lane l: column l % 32, row 8(v/4) + 4g + v%4; the
 // weight fragment is the first operand, so the accumulator's columns are
 // activation rows and its rows are output columns.
-#include <mutex>
 #include <type_traits>
 
 #include "abi_common.hpp"
@@ -1807,28 +1806,18 @@ constexpr int64_t kScratchTiles = 256;
 constexpr int64_t kScratchBytes = kScratchTiles * kPartialFloats * (int64_t)sizeof(float);
 static __device__ __align__(256) float scratch[kScratchTiles * kPartialFloats];
 
-// Device address of this GPU's `scratch`, looked up with the device current
-// on the first call made on it.  The host-side name is only a stand-in
-// handle: kernels get this address, never the name.
+// Device address of the current GPU's `scratch`, looked up on every call
+// with that device current: each GPU holds its own copy at its own address,
+// and a hipDeviceReset reloads the code object (a cached address would then
+// dangle).  The lookup is a host-side table query, small next to a GEMM
+// launch.  The host-side name is only a stand-in handle: kernels get this
+// address, never the name.
 static int32_t scratch_on_current_device(void **out) {
-  constexpr int kMaxDevices = 64;
-  static std::mutex mu;
-  static void *addr[kMaxDevices];
-  int dev = 0;
-  hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess) return fail(NF4S_ERR_HIP, "hipGetDevice: %s", hipGetErrorString(e));
-  if (dev < 0 || dev >= kMaxDevices)
-    return fail(NF4S_ERR_UNSUPPORTED_SHAPE, "device %d beyond the %d the scratch table holds",
-                dev, kMaxDevices);
-  std::lock_guard<std::mutex> lock(mu);
-  if (addr[dev] == nullptr) {
-    void *p = nullptr;
-    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-    if (e != hipSuccess || p == nullptr)
-      return fail(NF4S_ERR_HIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
-    addr[dev] = p;
-  }
-  *out = addr[dev];
+  void *p = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || p == nullptr)
+    return fail(NF4S_ERR_HIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+  *out = p;
   return NF4S_OK;
 }
 

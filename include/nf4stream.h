@@ -267,7 +267,12 @@ int32_t nf4s_gemm_fwd_workspace_size(const int64_t *ns, int32_t count, int64_t m
  * (possible only on devices with more than 256 CUs).  Every call on one GPU
  * shares that GPU's array: calls that overlap on one GPU (different streams
  * without ordering, or several host threads) race.  Results are bit-identical
- * to nf4s_gemm_fwd_grouped_ws with a large enough workspace.
+ * to nf4s_gemm_fwd_grouped_ws with a large enough workspace.  The array's
+ * device address is looked up on every call (valid across hipDeviceReset).
+ * Under HIP graph capture: make one call on the device (of any entry point)
+ * before capturing, so that the library's code object is already loaded
+ * there; the call itself issues only kernel launches (no memset), so a
+ * captured call replays correctly.
  */
 int32_t nf4s_gemm_fwd_grouped_noalloc(const uint16_t *x, const nf4s_tensor *ws,
                                       const int64_t *ns, uint16_t *const *ys,

@@ -84,3 +84,42 @@ def test_noalloc_without_split_matches_plain_forward():
                                          torch.cuda.current_stream().cuda_stream))
     torch.cuda.synchronize()
     assert torch.equal(out[0], ref[0])
+
+
+def test_noalloc_captured_in_a_graph_replays_bit_exact():
+    """The entry point under HIP graph capture (its callers' case): one eager
+    call first (loads the code object on this device), then the captured
+    call (split-K launch + fixup on the static scratch, no memset) is
+    replayed three times with new x contents written eagerly between the
+    replays; every replay equals the workspace entry point run eagerly on the
+    same x, bit for bit."""
+    lib = _lib.load()
+    ws = _weights([(640, 8192, True), (384, 8192, True)], 4)
+    m, k = 512, 8192
+    g = torch.Generator(device="cuda").manual_seed(20)
+    x = torch.randn(m, k, device="cuda", generator=g).to(torch.bfloat16)
+    d, ns, outs, ys = _args(ws, m)
+    assert _workspace_bytes(ns, len(ws), m, k) > 0, "the case must take the split-K path"
+    stream = torch.cuda.current_stream().cuda_stream
+    _lib.check(lib.nf4s_gemm_fwd_grouped_noalloc(x.data_ptr(), d, ns, ys, len(ws), m, k, stream))
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        _lib.check(lib.nf4s_gemm_fwd_grouped_noalloc(
+            x.data_ptr(), d, ns, ys, len(ws), m, k, torch.cuda.current_stream().cuda_stream))
+    for rep in range(3):
+        x.copy_(torch.randn(m, k, device="cuda", generator=g).to(torch.bfloat16))
+        for o in outs:
+            o.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        d2, ns2, ref, ys2 = _args(ws, m)
+        nbytes = _workspace_bytes(ns2, len(ws), m, k)
+        work = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+        _lib.check(lib.nf4s_gemm_fwd_grouped_ws(x.data_ptr(), d2, ns2, ys2, len(ws), m, k,
+                                                work.data_ptr(), nbytes, stream))
+        torch.cuda.synchronize()
+        for a, b in zip(outs, ref):
+            assert not torch.isnan(a).any(), f"replay {rep} left outputs unwritten"
+            assert torch.equal(a, b), f"replay {rep} differs from the eager call"
