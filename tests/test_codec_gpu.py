@@ -160,27 +160,30 @@ LAYER_7B = [("q", 4096, 4096), ("k", 4096, 4096), ("v", 4096, 4096), ("o", 4096,
 
 
 def test_config2_7b_layer_batch_dequant_dq():
-    # Benchmark config 2: the 7 matrices of a Llama-7B layer, double-quant, one
-    # grouped launch; every output element compared with the oracle.
+    # Benchmark config 2, pinned whole: the 7 matrices of a Llama-7B layer
+    # (202,375,168 elements), double-quant.  For every matrix the device's
+    # packed codes, uint8 absmax codes and fp32 group scales equal the
+    # oracle's quantize_nf4 + dq_encode of the same fp32 weights, and every
+    # element of the one grouped dequant launch equals the oracle's bf16
+    # dequant of its own codes.
     g = torch.Generator(device=DEV).manual_seed(2)
-    ws = []
+    ws, refs = [], []
     for i, (_, r, c) in enumerate(LAYER_7B):
         wf = torch.randn(r, c, device=DEV, generator=g) * 0.02
         w = nf4.quantize_weight(wf, double_quant=True)
-        # Codes of the first and last 64 rows against the oracle quantizer.
-        for rows in (slice(0, 64), slice(r - 64, r)):
-            xs = wf[rows].contiguous().cpu().numpy()
-            pk_ref, am_ref = oracle.quantize_nf4(xs)
-            start = rows.start * c // 2
-            np.testing.assert_array_equal(
-                w.packed[start:start + pk_ref.size].cpu().numpy(), pk_ref)
+        pk_ref, am_ref = oracle.quantize_nf4(wf.cpu().numpy())
         del wf
+        q_ref, s_ref = oracle.dq_encode(am_ref, 256)
+        np.testing.assert_array_equal(w.packed.cpu().numpy(), pk_ref)
+        np.testing.assert_array_equal(w.absmax_q.cpu().numpy(), q_ref)
+        np.testing.assert_array_equal(w.absmax_scale.cpu().numpy().view(np.uint32),
+                                      s_ref.view(np.uint32))
         ws.append(w)
+        refs.append((pk_ref, q_ref, s_ref))
     outs = nf4.dequant_batch(ws)
     torch.cuda.synchronize()
-    for w, o in zip(ws, outs):
-        am2 = oracle.dq_decode(w.absmax_q.cpu().numpy(), w.absmax_scale.cpu().numpy(), 256)
-        ref = oracle.dequant_bf16(w.packed.cpu().numpy(), am2, w.numel)
+    for w, o, (pk_ref, q_ref, s_ref) in zip(ws, outs, refs):
+        ref = oracle.dequant_bf16(pk_ref, oracle.dq_decode(q_ref, s_ref, 256), w.numel)
         np.testing.assert_array_equal(_bits16(o).reshape(-1), ref)
 
 
