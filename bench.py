@@ -7,6 +7,9 @@ an fp32 scale), one grouped launch per step, inputs resident in HBM.
 ``value`` = algorithmic bytes (packed + uint8 absmax + fp32 scales + bf16 out
 = 509,149,440 B) / average kernel time (HIP events on the launch stream), GB/s.
 
+"dequant_cold": the same launch with inputs that cannot be cache hits: 4
+distinct 7B layers (416 MB of NF4 inputs, beyond the 256 MB Infinity Cache)
+dequantized in rotation, with its own roofline fraction.
 "dequant_host_roundtrip": the same layer through the reference's host-slice
 API (fp32 absmax in, f16 out, both in pinned host memory): H2D + dequant + D2H
 per matrix on one stream, the PCIe-inclusive rate (never ``value``).
@@ -31,16 +34,21 @@ hipBLASLt) of the 70B gate shape on the same box, and what an unfused path
 (dequantize the layer to bf16, then that GEMM rate) would reach on config 4.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
-                       [--workload all|dequant|gemm|stream|quantize] [--stream-layers L]
+                       [--workload all|dequant|dequant-cold|gemm|stream|quantize]
+                       [--stream-layers L]
                        [--copy-calibration]
-                       [--gemm-shape NAME [--gemm-mode fwd|dgrad|wgrad|swiglu]]
+                       [--gemm-shape NAME [--gemm-mode fwd|dgrad|wgrad|swiglu] [--gemm-rotate R]]
+  --workload dequant-cold runs only the cold-input dequant leg and prints its
+  line (profiling).
   --workload quantize runs config 1 alone (oracle quantize on one core, then the
   device quantize of the same matrix) and prints only its line (profiling).
   --crossover times the 70B layer's forward and input-gradient passes fused and
   unfused at 256-8192 tokens and prints only that line.
   --gemm-shape times one fused GEMM (70b_q, 70b_k, 70b_gate, 70b_down, 7b_gate,
   7b_down) `steps` times after `warmup` and prints only its line (profiling);
-  --gemm-mode bf16-reference times torch.matmul in bf16 on that shape instead.
+  --gemm-mode bf16-reference times torch.matmul in bf16 on that shape instead;
+  --gemm-rotate R (forward) cycles R distinct weights of the shape, so that the
+  weight reads of a launch cannot be Infinity-Cache hits left by the last one.
 """
 from __future__ import annotations
 
@@ -89,7 +97,8 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="approximate CPU time budget of the dequant cpu_baseline sample")
-    ap.add_argument("--workload", choices=["all", "dequant", "gemm", "stream", "quantize"],
+    ap.add_argument("--workload", choices=["all", "dequant", "dequant-cold", "gemm", "stream",
+                                           "quantize"],
                     default="all")
     ap.add_argument("--crossover", action="store_true",
                     help="time the 70B layer's fused and unfused passes over token counts "
@@ -100,6 +109,9 @@ def parse():
                     help="only run a plain 1 GiB device-to-device copy (PMC byte calibration)")
     ap.add_argument("--gemm-shape", choices=sorted(GEMM_SHAPES), default=None,
                     help="only time one fused GEMM shape (for profiling)")
+    ap.add_argument("--gemm-rotate", type=int, default=1,
+                    help="with --gemm-shape and --gemm-mode fwd: cycle through this many "
+                         "distinct weights of the shape (weights beyond the Infinity Cache)")
     ap.add_argument("--gemm-mode", choices=["fwd", "dgrad", "wgrad", "swiglu", "bf16-reference"],
                     default="fwd",
                     help="wgrad: the weight gradient dW[n,k] = dy^T.x over m tokens (fp32 out); "
@@ -152,10 +164,10 @@ def timed(torch, fn, steps, warmup, warm_s=None, name=None):
     return start.elapsed_time(end) / steps
 
 
-def read_traffic():
-    """HBM bytes per dequant launch from the committed rocprofv3 PMC summary."""
+def read_traffic(path=TRAFFIC_FILE):
+    """HBM bytes per dequant launch from a committed rocprofv3 PMC summary."""
     try:
-        with open(TRAFFIC_FILE) as f:
+        with open(path) as f:
             for line in f:
                 if line.startswith("traffic_bytes_per_launch:"):
                     return int(float(line.split(":", 1)[1].strip()))
@@ -310,6 +322,45 @@ def bench_dequant(torch, nf4, args):
     ms = timed(torch, lambda: nf4.dequant_batch(ws, outs), args.steps, args.warmup,
                name="config2_dequant")
     return ws, ms
+
+
+COLD_LAYERS = 4
+COLD_TRAFFIC_FILE = os.path.join(ROOT, "profiles", "dequant_7b_cold_pmc.txt")
+
+
+def bench_dequant_cold(torch, nf4, args, ws0=None):
+    """The headline launch on inputs that cannot be cache hits: COLD_LAYERS
+    distinct 7B layers (each its own packed codes, absmax codes and scales,
+    104 MB; 416 MB together, beyond the 256 MB Infinity Cache) and as many
+    output sets, one layer per step in rotation, so every launch reads
+    inputs last touched COLD_LAYERS - 1 launches (1.5 GB of traffic) ago."""
+    log(f"cold-input dequant: {COLD_LAYERS} distinct 7B layers in rotation")
+    layers = [ws0] if ws0 is not None else []
+    while len(layers) < COLD_LAYERS:
+        layers.append(make_weights(torch, nf4, LAYER_7B, seed=20 + len(layers)))
+    outs = [[torch.empty(w.shape, dtype=torch.bfloat16, device="cuda") for w in ws]
+            for ws in layers]
+    it = [0]
+
+    def step():
+        i = it[0] % COLD_LAYERS
+        it[0] += 1
+        nf4.dequant_batch(layers[i], outs[i])
+
+    steps = max(COLD_LAYERS, (args.steps + COLD_LAYERS - 1) // COLD_LAYERS * COLD_LAYERS)
+    ms = timed(torch, step, steps, COLD_LAYERS, name="config2_dequant_cold")
+    nbytes = algorithmic_bytes_dq(LAYER_7B)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    in_bytes = sum(w.packed.numel() + w.absmax_q.numel() + 4 * w.absmax_scale.numel()
+                   for ws in layers for w in ws)
+    return {"gbs": round(gbs, 2), "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "us_per_launch": round(ms * 1e3, 2), "layers_rotated": COLD_LAYERS,
+            "input_bytes_rotated": in_bytes,
+            "output_bytes_rotated": sum(o.numel() * 2 for os_ in outs for o in os_),
+            "steps": steps, "traffic": read_traffic(COLD_TRAFFIC_FILE),
+            "note": "same grouped launch as value; each launch's inputs were last read "
+                    f"{COLD_LAYERS - 1} launches earlier, with 416 MB of other inputs and "
+                    "1.2 GB of other outputs in between"}
 
 
 def bench_dequant_host(torch, nf4, args):
@@ -631,7 +682,20 @@ def bench_one_gemm(torch, nf4, gemm, args):
     m, n, k = GEMM_SHAPES[args.gemm_shape]
     g = torch.Generator(device="cuda").manual_seed(7)
     w = nf4.quantize_weight(torch.randn(n, k, device="cuda", generator=g) * 0.02, double_quant=True)
-    if args.gemm_mode == "fwd":
+    if args.gemm_mode == "fwd" and args.gemm_rotate > 1:
+        # Distinct weights of the shape in rotation (--gemm-rotate): each
+        # launch reads NF4 bytes last read gemm_rotate - 1 launches earlier.
+        rot = [w] + [nf4.quantize_weight(torch.randn(n, k, device="cuda", generator=g) * 0.02,
+                                         double_quant=True)
+                     for _ in range(args.gemm_rotate - 1)]
+        a = torch.randn(m, k, device="cuda", generator=g).to(torch.bfloat16)
+        o = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
+        it = [0]
+
+        def fn():
+            gemm.linear_fwd(a, rot[it[0] % len(rot)], o)
+            it[0] += 1
+    elif args.gemm_mode == "fwd":
         a = torch.randn(m, k, device="cuda", generator=g).to(torch.bfloat16)
         o = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
         fn = lambda: gemm.linear_fwd(a, w, o)
@@ -659,7 +723,8 @@ def bench_one_gemm(torch, nf4, gemm, args):
     ms = timed(torch, fn, args.steps, args.warmup, name=f"{args.gemm_shape}_{args.gemm_mode}")
     tf = (4.0 if args.gemm_mode == "swiglu" else 2.0) * m * n * k / (ms * 1e-3) / 1e12
     print(json.dumps({"gemm_shape": args.gemm_shape, "mode": args.gemm_mode, "m": m, "n": n,
-                      "k": k, "ms": round(ms, 4), "tflops": round(tf, 1)}), flush=True)
+                      "k": k, "ms": round(ms, 4), "tflops": round(tf, 1),
+                      "weights_rotated": max(1, args.gemm_rotate)}), flush=True)
 
 
 def bench_crossover(torch, nf4, gemm, args):
@@ -812,6 +877,10 @@ def main():
                                                                      args),
                           "cpu_baseline_quantize_config1": leg}), flush=True)
         return
+    if args.workload == "dequant-cold":
+        # The cold-input leg alone (the program its counter runs profile).
+        print(json.dumps({"dequant_cold": bench_dequant_cold(torch, nf4, args)}), flush=True)
+        return
 
     line = {
         "metric": "NF4 dequant HBM GB/s (% peak); NF4-fused GEMM TFLOP/s at 7B/70B layer shapes",
@@ -838,6 +907,7 @@ def main():
         line["roofline"] = {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
                             "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
                             "traffic": read_traffic()}
+        line["dequant_cold"] = bench_dequant_cold(torch, nf4, args, ws)
         log("HBM copy ceiling")
         line["hbm_copy_ceiling"] = hbm_copy_ceiling(torch)
         log("PCIe-inclusive host-slice dequant")
