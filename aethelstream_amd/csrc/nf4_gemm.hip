@@ -146,19 +146,44 @@ struct PerStepLoads {
   }
 };
 
+// The product table of a block shared by the two lanes that dequantize it
+// (the two 32-element halves of one 64-element block): lane half h builds
+// table entries 8h .. 8h+7 (8 products, 4 conversions, 4 byte-plane perms,
+// half the work) and receives the other 8 from its partner by DPP.  Its table
+// registers then hold (own entries, partner's entries): entries 0-7 first on
+// an h = 0 lane, entries 8-15 first on an h = 1 lane.  The lookup picks the
+// table half by bit 3 of the nibble, so an h = 1 lane flips bit 3 of every
+// nibble of its packed words first (hmask): code c is looked up at c ^ 8,
+// where that lane keeps it.  Each product still depends on (code, absmax)
+// only, so every element keeps the reference's bits.
+struct HalfTable {
+  uint32_t hmask;  // 0x88888888 on an h = 1 lane, else 0
+  float code[8];   // NF4 codes 8h .. 8h+7
+  __device__ __forceinline__ void init_half(int h) {
+    hmask = h ? 0x88888888u : 0u;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) code[j] = h ? code_value(8 + j) : code_value(j);
+  }
+};
+
 // Forward producer: thread -> (row n_local, half h), 32 consecutive k of one
 // block; writes 4 swizzled 16-B units of its row.  Lanes 16j..16j+15 of a
-// wave take 16 consecutive rows at one half, so each 16-lane group of a
-// ds_write_b128 covers 16 rows at one logical unit (no bank conflicts).
-// FwdStore holds that mapping and the stores; the two forward producers
-// differ only in how the packed words and absmax reach the registers.
-struct FwdStore {
+// wave take 8 consecutive rows, lanes 16j..16j+7 their half 0 and lanes
+// 16j+8..16j+15 their half 1, so the two lanes of a block are 8 apart in one
+// 16-lane DPP row (row_ror:8 swaps them), and each 8-lane group of a
+// ds_write_b128 (a 128-B bank window) covers 8 consecutive rows at one
+// logical unit, 8 distinct physical units (no bank conflicts).  FwdStore
+// holds that mapping and the stores; the two forward producers differ only
+// in how the packed words and absmax reach the registers.
+struct FwdStore : HalfTable {
   static constexpr bool kFwd = true;
+  static constexpr int kDppPartner = 0x128;  // row_ror:8: lane ^ 8 within 16
   int row, h;
   __device__ __forceinline__ void init_row() {
     const int lane = threadIdx.x & 63;
-    row = 32 * (threadIdx.x >> 6) + 16 * (lane >> 5) + (lane & 15);
-    h = (lane >> 4) & 1;
+    row = 32 * (threadIdx.x >> 6) + 16 * (lane >> 5) + 8 * ((lane >> 4) & 1) + (lane & 7);
+    h = (lane >> 3) & 1;
+    init_half(h);
   }
   __device__ __forceinline__ float masked(float a) const { return a; }
   // Writes the 8 dequantized elements of packed word k (natural order).
@@ -220,10 +245,11 @@ struct FwdProducer : FwdStore, PerStepLoads<kDQ, FwdProducer<kDQ>> {
 // stream evicts those lines before the next step comes back to them.  So:
 //  * packed nibbles are loaded two steps at a time: instruction X covers the
 //    wave's rows 0-15 and instruction Y rows 16-31, 64 contiguous bytes per
-//    row (lane l: row l % 16, 16-B chunk l / 16 = (step 2p + c / 2, half
-//    c % 2)).  v_permlane32_swap then exchanges X's upper 32 lanes with Y's
-//    lower 32: X holds step 2p and Y step 2p+1, both in the thread -> (row,
-//    half) layout of FwdStore.  Half the cache lines per step.
+//    row (lane l: row 8 ((l / 16) % 2) + l % 8, 16-B chunk c = 2 (l / 32) +
+//    (l / 8) % 2 = (step 2p + c / 2, half c % 2)).  v_permlane32_swap then
+//    exchanges X's upper 32 lanes with Y's lower 32: X holds step 2p and Y
+//    step 2p+1, both in the thread -> (row, half) layout of FwdStore.  Half
+//    the cache lines per step.
 //  * absmax is loaded four steps at a time: one dword of double-quant codes
 //    (or one float4 of fp32 absmax) plus one scale per thread.  The four
 //    blocks lie in one scale group (dq_group >= 4, and 4 | blocks per row).
@@ -249,12 +275,13 @@ struct FwdBatchProducer : FwdStore {
     if (n >= g.wn) n = g.wn - 1;
     am_idx = n * (g.wk >> 6) + g.k0;  // absolute block: scale groups stay aligned
     am = g.am;
-    int64_t nx = n0 + 32 * (threadIdx.x >> 6) + (lane & 15);
+    int64_t nx = n0 + 32 * (threadIdx.x >> 6) + 8 * ((lane >> 4) & 1) + (lane & 7);
     int64_t ny = nx + 16;
     if (nx >= g.wn) nx = g.wn - 1;
     if (ny >= g.wn) ny = g.wn - 1;
-    pkx = g.packed + nx * (g.wk >> 1) + 16 * (lane >> 4) + 32 * g.k0;
-    pky = g.packed + ny * (g.wk >> 1) + 16 * (lane >> 4) + 32 * g.k0;
+    const int chunk = 2 * (lane >> 5) + ((lane >> 3) & 1);
+    pkx = g.packed + nx * (g.wk >> 1) + 16 * chunk + 32 * g.k0;
+    pky = g.packed + ny * (g.wk >> 1) + 16 * chunk + 32 * g.k0;
     npairs = (int)(g.R >> 7);
     ngroups = (int)(g.R >> 8);
   }
@@ -365,13 +392,16 @@ struct FwdBatchProducer : FwdStore {
 // DgradStore holds the thread mapping, the LDS stores and the transposed
 // fragment reads; the two input-gradient producers differ only in how the
 // packed words and absmax reach the registers.
-struct DgradStore {
+struct DgradStore : HalfTable {
   static constexpr bool kFwd = false;
+  static constexpr int kDppPartner = 0xB1;   // quad_perm [1,0,3,2]: lane ^ 1
   uint32_t valid_mask;  // all ones when the thread's columns exist
   int sidx[4];          // LDS unit of the thread's word k
   uint32_t roff[4];     // byte offset of the lane's read of fragment j (rows 0-3 of sub-step 0)
+  // Quarters 2b and 2b + 1 of a row are the two halves of its block b.
   __device__ void init_layout(const GemmArgs &g, int64_t o0) {
     const int r = threadIdx.x >> 2, q = threadIdx.x & 3, c = r & 3;
+    init_half(q & 1);
 #pragma unroll
     for (int k = 0; k < 4; ++k) sidx[k] = 16 * r + 4 * (q ^ c) + ((k ^ (2 * (q >> 1))) ^ c);
     const int lane = threadIdx.x & 63, l16 = lane & 15, cr = l16 >> 2;
@@ -577,8 +607,11 @@ __device__ __forceinline__ void read_frag(const Producer &prod, const u32x4 *__r
 // sub-step 3 has 8 slots before the barrier, so a step has 56.  Job kinds:
 //   R  two fragment reads of the next sub-step (slots 0-3 of sub-steps 0-2);
 //      'n' is R plus an N job
-//   M  one quarter of the product table (4 products, 2 conversions, the
-//      quarter's two low/high byte words)
+//   M  one quarter of this lane's half of the product table (2 products,
+//      1 conversion; the second and fourth also form the half-quarter's low /
+//      high byte words)
+//   D  the partner lane's half of the table, 4 DPP moves (after the 4 M jobs
+//      and before the first lookup stage that reads the table)
 //   W  one lookup stage of a packed word (NatLookup), in order: selectors,
 //      plane controls, elements 0-3, elements 4-7, the bf16 pairs, the
 //      16-B store
@@ -587,12 +620,14 @@ __device__ __forceinline__ void read_frag(const Producer &prod, const u32x4 *__r
 //   A  one activation DMA of the step after next (t+2), rows 0-63, into the
 //      current buffer once this wave's reads of it have returned
 //   .  the MFMA alone
-// Each slot holds about the issue time of one MFMA (32 cycles).  The last
-// weight-tile store (word 3's W stage 5) sits at slot 43, 12 slots before
-// the barrier, whose lgkmcnt(0) must see it complete; the A jobs follow in
-// the last 12 slots, after a wait for this wave's fragment reads only (the
-// LDS queue is in order, so the wait exempts the stores issued after the
-// last R slot).  N jobs go early: the barrier exempts only the 8 A jobs.
+// Each slot holds about the issue time of one MFMA (32 cycles), and an MFMA
+// hides about 5 independent VALU instructions: the table's 16 products go
+// in 4 slots of 3-5 instructions.  The last weight-tile store (word 3's W
+// stage 5) sits at slot 44, 11 slots before the barrier, whose lgkmcnt(0)
+// must see it complete; the A jobs follow in the last slots, after a wait
+// for this wave's fragment reads only (the LDS queue is in order, so the
+// wait exempts the stores issued after the last R slot).  N jobs go early:
+// the barrier exempts only the 8 A jobs.
 // On MI355X this plan measured +1.3 % (70B gate forward) to +3 % (70B q
 // input gradient) over one that stored the last word two slots before the
 // barrier; the 16 DMAs all in the second half of the step (16 exempt at the
@@ -602,9 +637,9 @@ __device__ __forceinline__ void read_frag(const Producer &prod, const u32x4 *__r
 // slots.
 constexpr int kDmaInFlight = 8;
 constexpr char kPlanFwd[57] =
-    "RnRnMMNMMNWWWWNN"
+    "RnRnMMNMMNDWWWNN"
     "RnRnWWWWWWWWWWWW"
-    "RRRRWWWWWWWW.A.A"
+    "RRRRWWWWWWWWWA.A"
     ".AAAAAA.";
 constexpr const char *kPlanDgrad = kPlanFwd;
 // Number of jobs of kind c before slot n ('n' counts as N).
@@ -628,18 +663,22 @@ constexpr int stores_after_reads(const char *plan, int n) {
   return stores;
 }
 // Shape of a plan: 56 slots; R/n at slots 0-3 of sub-steps 0-2; 8 N, 8 A, 24
-// W and 4 M jobs; the product table complete before the first lookup stage
-// that reads it (W stage 2 of word 0).
+// W, 4 M and 1 D jobs; the D job after the 4 M jobs and two slots after the
+// last (a DPP read of a register the previous VALU wrote needs wait states);
+// the product table complete before the first lookup stage that reads it (W
+// stage 2 of word 0).
 constexpr bool plan_ok(const char *plan) {
   int r = 0, w = 0;
   for (int i = 0; i < 56; ++i) {
     const bool rs = plan[i] == 'R' || plan[i] == 'n';
     if (rs != (i < 48 && i % 16 < 4)) return false;
     r += rs;
-    if (plan[i] == 'W' && w++ == 2 && plan_index(plan, i, 'M') != 4) return false;
+    if (plan[i] == 'D' && (plan_index(plan, i, 'M') != 4 || plan[i - 1] == 'M')) return false;
+    if (plan[i] == 'W' && w++ == 2 && plan_index(plan, i, 'D') != 1) return false;
   }
   return plan[56] == 0 && r == 12 && plan_index(plan, 56, 'N') == 8 &&
-         plan_index(plan, 56, 'A') == 8 && w == 24 && plan_index(plan, 56, 'M') == 4;
+         plan_index(plan, 56, 'A') == 8 && w == 24 && plan_index(plan, 56, 'M') == 4 &&
+         plan_index(plan, 56, 'D') == 1;
 }
 static_assert(plan_ok(kPlanFwd), "forward slot plan");
 static_assert(plan_ok(kPlanDgrad), "input-gradient slot plan");
@@ -680,6 +719,7 @@ __device__ __forceinline__ void gemm_step(const GemmArgs &g, Producer &prod,
   const int t2 = (t + 2 < nsteps) ? t + 2 : nsteps - 1;
   Lut16 lut;
   uint32_t lutd[2];
+  uint32_t own[4];  // this lane's half: low / high byte words of its 2 quarters
   NatLookup wl;
   uint32_t wp[4][4];  // dequantized elements of each packed word, memory order
   float ta = 0.0f;
@@ -725,16 +765,33 @@ __device__ __forceinline__ void gemm_step(const GemmArgs &g, Producer &prod,
       dma(Acur, d, t2);
     }
     if constexpr (kind == 'M') {
-      // One quarter of the product table (two halves).
-      constexpr int h = 2 * plan_index(kFwd ? kPlanFwd : kPlanDgrad, n, 'M');
-      make_lut_half<false>(ta, h, lutd, lut);
-      make_lut_half<false>(ta, h + 1, lutd, lut);
+      // Entries 2j and 2j+1 of this lane's half of the table.
+      constexpr int j = plan_index(kFwd ? kPlanFwd : kPlanDgrad, n, 'M');
+      const float p0 = fp32_rounded(prod.code[2 * j] * ta);
+      const float p1 = fp32_rounded(prod.code[2 * j + 1] * ta);
+      lutd[j & 1] = pack_bf16x2(p0, p1);
+      if constexpr (j & 1) {
+        own[2 * (j >> 1)] = perm(lutd[1], lutd[0], 0x06040200u);
+        own[2 * (j >> 1) + 1] = perm(lutd[1], lutd[0], 0x07050301u);
+      }
+    }
+    if constexpr (kind == 'D') {
+      // (own half, partner's half): see HalfTable.
+      static_for<0, 2>([&](auto Q) {
+        constexpr int q = decltype(Q)::value;
+        lut.lo[q] = own[2 * q];
+        lut.hi[q] = own[2 * q + 1];
+        lut.lo[2 + q] = (uint32_t)__builtin_amdgcn_mov_dpp((int)own[2 * q], Producer::kDppPartner,
+                                                           0xf, 0xf, false);
+        lut.hi[2 + q] = (uint32_t)__builtin_amdgcn_mov_dpp((int)own[2 * q + 1],
+                                                           Producer::kDppPartner, 0xf, 0xf, false);
+      });
     }
     if constexpr (kind == 'W') {
       constexpr int j = plan_index(kFwd ? kPlanFwd : kPlanDgrad, n, 'W');
       constexpr int k = j / kWordStages, stage = j % kWordStages;
       if constexpr (stage == 0) {
-        nat_select(prod.template word<kPhase>(k), wl);
+        nat_select(prod.template word<kPhase>(k) ^ prod.hmask, wl);
       } else if constexpr (stage == 1) {
         nat_controls(wl);
       } else if constexpr (stage == 2) {
