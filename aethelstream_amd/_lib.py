@@ -68,6 +68,8 @@ class Nf4sReadyLayer(ctypes.Structure):
         ("slab_device_ptr", ctypes.c_void_p),
         ("bytes", ctypes.c_int64),
         ("copy_event", ctypes.c_void_p),
+        ("precision", ctypes.c_int32),
+        ("needs_decode", ctypes.c_int32),
     ]
 
 
@@ -134,6 +136,13 @@ SIGNATURES = {
     "nf4s_stream_wait_event": (_I32, [_P, _P]),
     "nf4s_take_ready": (_I32, [_P, ctypes.c_uint32, _P, _I64, ctypes.POINTER(Nf4sReadyLayer)]),
     "nf4s_retire_layer": (_I32, [_P, ctypes.POINTER(Nf4sReadyLayer), _P]),
+    "nf4s_residency_create": (_I32, [ctypes.c_uint32, ctypes.POINTER(_P)]),
+    "nf4s_residency_destroy": (_I32, [_P]),
+    "nf4s_residency_publish": (_I32, [_P, ctypes.c_uint32, _P, _I64, _I32]),
+    "nf4s_residency_wait": (_I32, [_P, ctypes.c_uint32, _I64, ctypes.POINTER(_P),
+                                   ctypes.POINTER(_I64), ctypes.POINTER(_I32)]),
+    "nf4s_take_ready_wait": (_I32, [_P, _P, ctypes.c_uint32, _I64,
+                                    ctypes.POINTER(Nf4sReadyLayer)]),
     "nf4s_loader_open": (_I32, [ctypes.c_char_p, ctypes.POINTER(_P)]),
     "nf4s_loader_close": (_I32, [_P]),
     "nf4s_loader_param_info": (_I32, [_P, ctypes.c_char_p, ctypes.POINTER(Nf4sParamInfo)]),

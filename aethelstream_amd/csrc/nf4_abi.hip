@@ -75,6 +75,7 @@ const char *nf4s_strerror(int32_t status) {
     case NF4S_ERR_LAYER_NOT_FOUND: return "layer index not found in layer registry";
     case NF4S_ERR_PARAM_NOT_FOUND: return "parameter not found in shard index";
     case NF4S_ERR_MALFORMED_INDEX: return "malformed index entry";
+    case NF4S_ERR_PREFETCH_MISS: return "prefetch miss";
     default: return "unknown status";
   }
 }

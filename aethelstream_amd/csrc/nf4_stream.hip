@@ -16,7 +16,11 @@
 // event the copy stream waits on, so the host may run ahead of the GPU.
 #include "abi_common.hpp"
 
+#include <chrono>
+#include <condition_variable>
+#include <mutex>
 #include <new>
+#include <vector>
 
 struct nf4s_dbuf {
   void *slot[2];          // device buffers
@@ -28,6 +32,21 @@ struct nf4s_dbuf {
   int64_t capacity;
   int staging;            // index of slot_b (the next copy target)
   hipStream_t copy;
+};
+
+// The ready map of FlowCast's prefetch state machine
+// (flowcast/src/state_machine.rs:306-346): per layer, the pinned blob a
+// prefetcher published and its precision, until take_ready takes it.
+struct nf4s_residency {
+  struct Entry {
+    bool resident = false;
+    const void *pinned = nullptr;
+    int64_t bytes = 0;
+    int32_t precision = 0;
+  };
+  std::mutex mu;
+  std::condition_variable cv;
+  std::vector<Entry> layers;
 };
 
 namespace nf4s {
@@ -174,6 +193,99 @@ int32_t nf4s_take_ready(nf4s_dbuf *d, uint32_t layer_idx, const void *pinned, in
   out->slab_device_ptr = ptr;
   out->bytes = len;
   out->copy_event = ev;
+  out->precision = NF4S_PRECISION_NF4;
+  out->needs_decode = 0;
+  return NF4S_OK;
+}
+
+int32_t nf4s_residency_create(uint32_t num_layers, nf4s_residency **out) {
+  clear_error();
+  if (out == nullptr) return fail(NF4S_ERR_INVALID_ARGUMENT, "out is NULL");
+  *out = nullptr;
+  try {
+    nf4s_residency *r = new nf4s_residency();
+    r->layers.resize(num_layers);
+    *out = r;
+  } catch (...) {
+    return fail(NF4S_ERR_INVALID_ARGUMENT, "out of host memory");
+  }
+  return NF4S_OK;
+}
+
+int32_t nf4s_residency_destroy(nf4s_residency *r) {
+  clear_error();
+  delete r;
+  return NF4S_OK;
+}
+
+int32_t nf4s_residency_publish(nf4s_residency *r, uint32_t layer_idx, const void *pinned,
+                               int64_t bytes, int32_t precision) {
+  clear_error();
+  if (r == nullptr) return fail(NF4S_ERR_INVALID_ARGUMENT, "residency is NULL");
+  if (bytes < 0 || (bytes > 0 && pinned == nullptr))
+    return fail(NF4S_ERR_INVALID_ARGUMENT, "bad blob for layer %u", layer_idx);
+  if (precision < NF4S_PRECISION_FP32 || precision > NF4S_PRECISION_NF4)
+    return fail(NF4S_ERR_INVALID_ARGUMENT, "unknown precision %d", precision);
+  {
+    std::lock_guard<std::mutex> lock(r->mu);
+    if (layer_idx >= r->layers.size())
+      return fail(NF4S_ERR_LAYER_NOT_FOUND, "layer %u beyond the %zu the table holds", layer_idx,
+                  r->layers.size());
+    nf4s_residency::Entry &e = r->layers[layer_idx];
+    if (e.resident) return fail(NF4S_ERR_INVALID_ARGUMENT, "layer %u is already resident", layer_idx);
+    e.resident = true;
+    e.pinned = pinned;
+    e.bytes = bytes;
+    e.precision = precision;
+  }
+  r->cv.notify_all();
+  return NF4S_OK;
+}
+
+// state_machine.rs:306-324: the deadline is tested first on every pass,
+// then readiness; a ready layer is taken (removed from the map).
+int32_t nf4s_residency_wait(nf4s_residency *r, uint32_t layer_idx, int64_t timeout_us,
+                            const void **pinned, int64_t *bytes, int32_t *precision) {
+  clear_error();
+  if (r == nullptr || pinned == nullptr || bytes == nullptr || precision == nullptr)
+    return fail(NF4S_ERR_INVALID_ARGUMENT, "bad residency_wait args");
+  if (timeout_us < 0) return fail(NF4S_ERR_INVALID_ARGUMENT, "negative timeout");
+  using clock = std::chrono::steady_clock;
+  const clock::time_point start = clock::now();
+  const clock::time_point deadline = start + std::chrono::microseconds(timeout_us);
+  std::unique_lock<std::mutex> lock(r->mu);
+  if (layer_idx >= r->layers.size())
+    return fail(NF4S_ERR_LAYER_NOT_FOUND, "layer %u beyond the %zu the table holds", layer_idx,
+                r->layers.size());
+  for (;;) {
+    if (clock::now() >= deadline)
+      return fail(NF4S_ERR_PREFETCH_MISS, "prefetch miss on layer %u", layer_idx);
+    nf4s_residency::Entry &e = r->layers[layer_idx];
+    if (e.resident) {
+      e.resident = false;
+      *pinned = e.pinned;
+      *bytes = e.bytes;
+      *precision = e.precision;
+      return NF4S_OK;
+    }
+    r->cv.wait_until(lock, deadline);
+  }
+}
+
+int32_t nf4s_take_ready_wait(nf4s_dbuf *d, nf4s_residency *r, uint32_t layer_idx,
+                             int64_t timeout_us, nf4s_ready_layer *out) {
+  clear_error();
+  if (d == nullptr || out == nullptr) return fail(NF4S_ERR_INVALID_ARGUMENT, "bad take_ready args");
+  const void *pinned = nullptr;
+  int64_t bytes = 0;
+  int32_t precision = 0;
+  int32_t rc = nf4s_residency_wait(r, layer_idx, timeout_us, &pinned, &bytes, &precision);
+  if (rc != NF4S_OK) return rc;
+  rc = nf4s_take_ready(d, layer_idx, pinned, bytes, out);
+  if (rc != NF4S_OK) return rc;
+  out->precision = precision;
+  // QuantizedDecoder::needs_decode (flowcast/src/decode.rs:181-183).
+  out->needs_decode = (precision == NF4S_PRECISION_INT4 || precision == NF4S_PRECISION_INT8);
   return NF4S_OK;
 }
 

@@ -13,11 +13,15 @@ double-quant absmax codes and fp32 scales, each segment 256-byte aligned
 
 ``FlowCastSeam`` is the hand-off of FlowCast's cuda-double-buffer path
 (flowcast/src/lib.rs:458-545, ready.rs:20-52): blobs packed by the shard
-loader from the on-disk NF4 payloads (``ShardLoader.pack_layer``) wait in
-pinned memory, ``take_ready`` copies one into the double buffer and returns a
-``ReadyLayer`` (slab 0 = the slot, plus the copy event), ``retire_layer``
-releases it.  Only the seam: no prefetch state machine and no file I/O
-backend (a blob is packed when first asked for).
+loader from the on-disk NF4 payloads (``ShardLoader.pack_layer``) are made
+resident in pinned memory and published (``prefetch``, the completion side
+of FlowCast's prefetch state machine; any thread may call it),
+``take_ready`` blocks until the layer is resident or its timeout passes
+(``PrefetchMiss``, flowcast/src/error.rs:20-25), copies it into the double
+buffer and returns a ``ReadyLayer`` (slab 0 = the slot, the copy event, the
+layer's precision and needs_decode), ``retire_layer`` releases it.  The
+prefetch policy itself and the file I/O backend are not built: ``prefetch``
+packs the blob in the calling thread.
 """
 from __future__ import annotations
 
@@ -202,18 +206,78 @@ class BlobLayout:
         return out
 
 
+# enum nf4s_precision: flowcast/src/config.rs:16-27 Precision, plus NF4.
+PRECISIONS = ("FP32", "FP16", "BF16", "INT8", "INT4", "NF4")
+PRECISION_NF4 = PRECISIONS.index("NF4")
+NF4S_ERR_PREFETCH_MISS = 12
+
+
+class PrefetchMiss(Exception):
+    """``FlowCastError::PrefetchMiss { layer_idx }`` (flowcast/src/error.rs:
+    20-25): the layer was not resident before take_ready's timeout."""
+
+    def __init__(self, layer_idx: int, message: str):
+        super().__init__(message)
+        self.layer_idx = layer_idx
+
+
+class Residency:
+    """The ready map of FlowCast's prefetch state machine
+    (flowcast/src/state_machine.rs:306-346): layers a prefetcher published as
+    resident in pinned memory, each taken once by a waiter (nf4s_residency_*).
+    Thread-safe; a waiting call releases the GIL."""
+
+    def __init__(self, num_layers: int):
+        h = ctypes.c_void_p()
+        _lib.check(_lib.load().nf4s_residency_create(int(num_layers), ctypes.byref(h)))
+        self.handle = h
+
+    def publish(self, layer_idx: int, ptr: int, nbytes: int, precision: int = PRECISION_NF4):
+        _lib.check(_lib.load().nf4s_residency_publish(self.handle, int(layer_idx), ptr,
+                                                      int(nbytes), int(precision)))
+
+    def wait(self, layer_idx: int, timeout: float) -> Tuple[int, int, int]:
+        """(pinned pointer, bytes, precision) of the layer once resident;
+        ``PrefetchMiss`` after ``timeout`` seconds (0 always misses, as the
+        reference checks the deadline first)."""
+        p, nb, pr = ctypes.c_void_p(), ctypes.c_int64(), ctypes.c_int32()
+        lib = _lib.load()
+        rc = lib.nf4s_residency_wait(self.handle, int(layer_idx), int(timeout * 1e6),
+                                     ctypes.byref(p), ctypes.byref(nb), ctypes.byref(pr))
+        if rc == NF4S_ERR_PREFETCH_MISS:
+            raise PrefetchMiss(layer_idx, lib.nf4s_last_error_message().decode())
+        _lib.check(rc)
+        return int(p.value or 0), int(nb.value), int(pr.value)
+
+    def close(self) -> None:
+        if self.handle:
+            _lib.check(_lib.load().nf4s_residency_destroy(self.handle))
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 @dataclass
 class ReadyLayer:
     """flowcast/src/ready.rs:20-52 with the cuda-double-buffer feature:
     ``slab_device_ptrs`` holds (0, slot pointer); the consumer waits on
     ``copy_event`` (``stream_wait_event``) before reading the slot, and hands
-    the layer back with ``FlowCastSeam.retire_layer``."""
+    the layer back with ``FlowCastSeam.retire_layer``.  ``precision`` is the
+    precision the blob was published in; ``needs_decode`` is True for INT4 /
+    INT8 (QuantizedDecoder::needs_decode, flowcast/src/decode.rs:181-183), so
+    False for NF4, which the fused GEMMs dequantize in-kernel."""
 
     layer_idx: int
     slab_device_ptrs: List[Tuple[int, int]]
     copy_event: int
     views: List[Nf4View]
     raw: _lib.Nf4sReadyLayer
+    precision: str = "NF4"
+    needs_decode: bool = False
 
 
 class FlowCastSeam:
@@ -238,6 +302,7 @@ class FlowCastSeam:
         self.pinned: Dict[int, PinnedBuffer] = {}
         cap = max((x.nbytes for x in self.layouts.values()), default=0)
         self.dbuf = VramDoubleBuffer(max(cap, 1))
+        self.residency = Residency(max(self.layouts, default=-1) + 1)
 
     def pin(self, layer_idx: int) -> PinnedBuffer:
         """The layer's blob in pinned memory, packed from the shards on first use."""
@@ -250,16 +315,30 @@ class FlowCastSeam:
             self.pinned[layer_idx] = pb
         return pb
 
-    def take_ready(self, layer_idx: int) -> ReadyLayer:
-        """Issues the layer's H2D copy on the copy stream; returns the ReadyLayer."""
-        lay = self.layouts[layer_idx]
+    def prefetch(self, layer_idx: int) -> None:
+        """Makes the layer resident (its blob packed into pinned memory on
+        first use) and publishes it to the ready map: the completion of a
+        prefetch in FlowCast's state machine.  Any thread may call it."""
         pb = self.pin(layer_idx)
+        self.residency.publish(layer_idx, pb.ptr, self.layouts[layer_idx].nbytes, PRECISION_NF4)
+
+    def take_ready(self, layer_idx: int, timeout: float = 0.5) -> ReadyLayer:
+        """FlowCast::take_ready (flowcast/src/lib.rs:458-498): blocks until
+        the layer is resident (``PrefetchMiss`` after ``timeout`` seconds;
+        0.5 s is wait_for_layer's default, lib.rs:531-533), takes it, issues
+        its H2D copy on the copy stream and returns the ReadyLayer."""
+        lay = self.layouts[layer_idx]
         raw = _lib.Nf4sReadyLayer()
-        _lib.check(_lib.load().nf4s_take_ready(self.dbuf.handle, layer_idx, pb.ptr, lay.nbytes,
-                                               ctypes.byref(raw)))
+        lib = _lib.load()
+        rc = lib.nf4s_take_ready_wait(self.dbuf.handle, self.residency.handle, layer_idx,
+                                      int(timeout * 1e6), ctypes.byref(raw))
+        if rc == NF4S_ERR_PREFETCH_MISS:
+            raise PrefetchMiss(layer_idx, lib.nf4s_last_error_message().decode())
+        _lib.check(rc)
         return ReadyLayer(layer_idx=layer_idx, slab_device_ptrs=[(0, raw.slab_device_ptr)],
                           copy_event=raw.copy_event, views=lay.views(raw.slab_device_ptr),
-                          raw=raw)
+                          raw=raw, precision=PRECISIONS[raw.precision],
+                          needs_decode=bool(raw.needs_decode))
 
     def retire_layer(self, layer: ReadyLayer, stream: torch.cuda.Stream) -> None:
         """The work enqueued so far on `stream` is the layer's last use."""
@@ -268,23 +347,34 @@ class FlowCastSeam:
 
     def close(self) -> None:
         self.dbuf.close()
+        self.residency.close()
         for pb in self.pinned.values():
             pb.close()
         self.pinned.clear()
 
 
 def stream_layers(seam: FlowCastSeam, order: Sequence[int], compute,
-                  stream: torch.cuda.Stream) -> None:
+                  stream: torch.cuda.Stream, prefetch: bool = True,
+                  timeout: float = 0.5) -> None:
     """The consumer loop of the double pass over the seam: the next layer's
     copy is issued before the current layer's kernels, the compute stream
     waits on each copy event, and each layer retires after its kernels.
-    ``compute(layer_idx, views)`` enqueues the kernels on the current stream."""
+    ``compute(layer_idx, views)`` enqueues the kernels on the current stream.
+    With ``prefetch`` (the default) each layer is published here just before
+    it is taken; without it another thread publishes them (``seam.prefetch``)
+    and ``take_ready`` waits up to ``timeout`` seconds for each."""
     order = list(order)
     if not order:
         return
-    cur = seam.take_ready(order[0])
+
+    def take(l):
+        if prefetch:
+            seam.prefetch(l)
+        return seam.take_ready(l, timeout)
+
+    cur = take(order[0])
     for i, l in enumerate(order):
-        nxt = seam.take_ready(order[i + 1]) if i + 1 < len(order) else None
+        nxt = take(order[i + 1]) if i + 1 < len(order) else None
         stream_wait_event(stream, cur.copy_event)
         with torch.cuda.stream(stream):
             compute(l, cur.views)

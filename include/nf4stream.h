@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define NF4S_ABI_VERSION 2
+#define NF4S_ABI_VERSION 3
 
 enum nf4s_status {
     NF4S_OK = 0,
@@ -41,7 +41,18 @@ enum nf4s_status {
     NF4S_ERR_JSON = 8,               /* error.rs:11-13 ShardEngineError::Json */
     NF4S_ERR_LAYER_NOT_FOUND = 9,    /* error.rs:15-17 ShardEngineError::LayerNotFound */
     NF4S_ERR_PARAM_NOT_FOUND = 10,   /* error.rs:19-21 ShardEngineError::ParamNotFound */
-    NF4S_ERR_MALFORMED_INDEX = 11    /* error.rs:23-25 MalformedIndex (index entries) */
+    NF4S_ERR_MALFORMED_INDEX = 11,   /* error.rs:23-25 MalformedIndex (index entries) */
+    NF4S_ERR_PREFETCH_MISS = 12      /* flowcast/src/error.rs:20-25 FlowCastError::PrefetchMiss */
+};
+
+/* flowcast/src/config.rs:16-27 Precision, plus the NF4 of this path. */
+enum nf4s_precision {
+    NF4S_PRECISION_FP32 = 0,
+    NF4S_PRECISION_FP16 = 1,
+    NF4S_PRECISION_BF16 = 2,
+    NF4S_PRECISION_INT8 = 3,
+    NF4S_PRECISION_INT4 = 4,
+    NF4S_PRECISION_NF4 = 5
 };
 
 /*
@@ -368,14 +379,48 @@ typedef struct nf4s_ready_layer {
     void *slab_device_ptr;   /* slab 0 (ready.rs:32-36) */
     int64_t bytes;           /* blob bytes copied into the slot */
     void *copy_event;        /* hipEvent_t (ready.rs:43-51) */
+    int32_t precision;       /* an nf4s_precision value; ready.rs:25-26 */
+    int32_t needs_decode;    /* 1 for INT4 / INT8 (ready.rs:38-41, decode.rs:181-183) */
 } nf4s_ready_layer;
 
-/* FlowCast::take_ready (flowcast/src/lib.rs:458-498) over the double buffer:
- * nf4s_dbuf_advance of the layer's pinned blob, returned as a ReadyLayer.
- * Fails like nf4s_dbuf_advance (capacity; a staging slot whose previous
- * layer was not retired). */
+/* FlowCast::take_ready (flowcast/src/lib.rs:458-498) over the double buffer,
+ * for a blob the caller holds resident: nf4s_dbuf_advance of the layer's
+ * pinned blob, returned as a ReadyLayer of precision NF4 (needs_decode 0:
+ * the fused GEMMs dequantize in-kernel).  Fails like nf4s_dbuf_advance
+ * (capacity; a staging slot whose previous layer was not retired). */
 int32_t nf4s_take_ready(nf4s_dbuf *d, uint32_t layer_idx, const void *pinned,
                         int64_t len, nf4s_ready_layer *out);
+
+/*
+ * Residency table: the layers whose blobs a prefetcher has made resident in
+ * pinned host memory, the ready map of FlowCast's prefetch state machine
+ * (flowcast/src/state_machine.rs:306-346 is_ready / take_slot).  Host-only
+ * and thread-safe: one thread may publish while another waits.
+ */
+typedef struct nf4s_residency nf4s_residency;
+int32_t nf4s_residency_create(uint32_t num_layers, nf4s_residency **out);
+int32_t nf4s_residency_destroy(nf4s_residency *r);
+/* Marks layer `layer_idx` resident: its blob is `bytes` at `pinned`, decoded
+ * in `precision`.  Wakes a waiter.  Fails for an index beyond the table or a
+ * layer already resident (not yet taken). */
+int32_t nf4s_residency_publish(nf4s_residency *r, uint32_t layer_idx,
+                               const void *pinned, int64_t bytes,
+                               int32_t precision);
+/* The state machine's take_ready (state_machine.rs:306-346): waits until the
+ * layer is resident, then takes it (a second wait for it waits for the next
+ * publish).  As the reference, the deadline is checked before readiness, so
+ * timeout_us = 0 always misses; past the deadline it returns
+ * NF4S_ERR_PREFETCH_MISS with the message "prefetch miss on layer N". */
+int32_t nf4s_residency_wait(nf4s_residency *r, uint32_t layer_idx,
+                            int64_t timeout_us, const void **pinned,
+                            int64_t *bytes, int32_t *precision);
+
+/* FlowCast::take_ready (flowcast/src/lib.rs:458-498) in full:
+ * nf4s_residency_wait, then nf4s_dbuf_advance of the taken blob.  The
+ * ReadyLayer carries the published precision and needs_decode =
+ * (precision is INT4 or INT8), as QuantizedDecoder::needs_decode. */
+int32_t nf4s_take_ready_wait(nf4s_dbuf *d, nf4s_residency *r, uint32_t layer_idx,
+                             int64_t timeout_us, nf4s_ready_layer *out);
 
 /* FlowCast::retire_layer (flowcast/src/lib.rs:543-545): the work enqueued so
  * far on `compute_stream` is the layer's last use (nf4s_dbuf_release of its

@@ -14,7 +14,7 @@
 
 use std::os::raw::{c_char, c_void};
 
-pub const NF4S_ABI_VERSION: i32 = 2;
+pub const NF4S_ABI_VERSION: i32 = 3;
 
 pub const NF4S_OK: i32 = 0;
 pub const NF4S_ERR_INVALID_ARGUMENT: i32 = 1;
@@ -28,6 +28,15 @@ pub const NF4S_ERR_JSON: i32 = 8;
 pub const NF4S_ERR_LAYER_NOT_FOUND: i32 = 9;
 pub const NF4S_ERR_PARAM_NOT_FOUND: i32 = 10;
 pub const NF4S_ERR_MALFORMED_INDEX: i32 = 11;
+pub const NF4S_ERR_PREFETCH_MISS: i32 = 12;
+
+/// `enum nf4s_precision`: flowcast/src/config.rs:16-27 Precision, plus NF4.
+pub const NF4S_PRECISION_FP32: i32 = 0;
+pub const NF4S_PRECISION_FP16: i32 = 1;
+pub const NF4S_PRECISION_BF16: i32 = 2;
+pub const NF4S_PRECISION_INT8: i32 = 3;
+pub const NF4S_PRECISION_INT4: i32 = 4;
+pub const NF4S_PRECISION_NF4: i32 = 5;
 
 /// `struct nf4s_tensor`: one NF4 tensor resident in device memory.
 #[repr(C)]
@@ -70,6 +79,8 @@ pub struct Nf4sReadyLayer {
     pub slab_device_ptr: *mut c_void,
     pub bytes: i64,
     pub copy_event: *mut c_void,
+    pub precision: i32,
+    pub needs_decode: i32,
 }
 
 /// `struct nf4s_blob_entry`: one parameter's parts inside a layer blob.
@@ -89,6 +100,12 @@ pub struct Nf4sBlobEntry {
 /// Opaque `nf4s_dbuf` (VRAM double buffer).
 #[repr(C)]
 pub struct Nf4sDbuf {
+    _private: [u8; 0],
+}
+
+/// Opaque `nf4s_residency` (the prefetch state machine's ready map).
+#[repr(C)]
+pub struct Nf4sResidency {
     _private: [u8; 0],
 }
 
@@ -171,6 +188,15 @@ extern "C" {
                              compute_stream: *mut c_void) -> i32;
     pub fn nf4s_take_ready(d: *mut Nf4sDbuf, layer_idx: u32, pinned: *const c_void, len: i64,
                            out: *mut Nf4sReadyLayer) -> i32;
+    pub fn nf4s_residency_create(num_layers: u32, out: *mut *mut Nf4sResidency) -> i32;
+    pub fn nf4s_residency_destroy(r: *mut Nf4sResidency) -> i32;
+    pub fn nf4s_residency_publish(r: *mut Nf4sResidency, layer_idx: u32, pinned: *const c_void,
+                                  bytes: i64, precision: i32) -> i32;
+    pub fn nf4s_residency_wait(r: *mut Nf4sResidency, layer_idx: u32, timeout_us: i64,
+                               pinned: *mut *const c_void, bytes: *mut i64,
+                               precision: *mut i32) -> i32;
+    pub fn nf4s_take_ready_wait(d: *mut Nf4sDbuf, r: *mut Nf4sResidency, layer_idx: u32,
+                                timeout_us: i64, out: *mut Nf4sReadyLayer) -> i32;
     pub fn nf4s_retire_layer(d: *mut Nf4sDbuf, layer: *const Nf4sReadyLayer,
                              compute_stream: *mut c_void) -> i32;
     pub fn nf4s_stream_wait_event(stream: *mut c_void, event: *mut c_void) -> i32;

@@ -14,7 +14,8 @@ BASE = {"int32_t": "i32", "int64_t": "i64", "uint32_t": "u32", "uint16_t": "u16"
         "uint8_t": "u8", "float": "f32", "char": "c_char", "void": "c_void",
         "nf4s_tensor": "Nf4sTensor", "nf4s_param_info": "Nf4sParamInfo",
         "nf4s_dbuf": "Nf4sDbuf", "nf4s_loader": "Nf4sLoader",
-        "nf4s_ready_layer": "Nf4sReadyLayer", "nf4s_blob_entry": "Nf4sBlobEntry"}
+        "nf4s_ready_layer": "Nf4sReadyLayer", "nf4s_blob_entry": "Nf4sBlobEntry",
+        "nf4s_residency": "Nf4sResidency"}
 
 
 def c_to_rust(ctype: str) -> str:
@@ -93,7 +94,7 @@ def test_status_constants_and_version():
     h = open(HEADER).read()
     rs = open(RUST).read()
     consts = dict(re.findall(r"(NF4S_\w+)\s*=\s*(\d+)", h))
-    assert len(consts) == 12
+    assert len(consts) == 19  # 13 status codes, 6 precisions
     for k, v in consts.items():
         assert re.search(rf"pub const {k}: i32 = {v};", rs), k
     ver = re.search(r"#define NF4S_ABI_VERSION (\d+)", h).group(1)

@@ -1,4 +1,7 @@
 """Streamed layer stack (flowcast VramDoubleBuffer semantics) on the GPU."""
+import threading
+import time
+
 import pytest
 import torch
 
@@ -150,9 +153,47 @@ def test_flowcast_seam_streams_shard_layers(tmp_path):
     for l in range(n):
         for a, b in zip(got[l], ref[l]):
             assert torch.equal(a, b), f"layer {l} differs"
+    # The same double pass with the layers published by another thread (the
+    # prefetcher side of take_ready), each at most one layer ahead and after
+    # a delay: take_ready blocks until the layer is resident.
+    for outs in got:
+        for o in outs:
+            o.fill_(float("nan"))
+    seen.clear()
+    taken = [0]
+    lock = threading.Condition()
+
+    def prefetcher():
+        for i, l in enumerate(order):
+            with lock:
+                lock.wait_for(lambda: taken[0] >= i - 1, timeout=10)
+            time.sleep(0.002)
+            seam.prefetch(l)
+
+    def compute2(l, views):
+        compute(l, views)
+        with lock:
+            taken[0] += 1
+            lock.notify_all()
+
+    th = threading.Thread(target=prefetcher)
+    th.start()
+    st.stream_layers(seam, order, compute2, stream, prefetch=False, timeout=10.0)
+    th.join()
+    torch.cuda.synchronize()
+    assert seen == order
+    for l in range(n):
+        for a, b in zip(got[l], ref[l]):
+            assert torch.equal(a, b), f"layer {l} differs (prefetcher thread)"
+    # A layer nobody published: PrefetchMiss after the timeout.
+    with pytest.raises(st.PrefetchMiss, match="prefetch miss on layer 4"):
+        seam.take_ready(4, timeout=0.02)
     # Protocol errors: a second retire, and a take_ready into a slot whose
     # layer was never retired.
+    for l in (0, 1, 2, 3):
+        seam.prefetch(l)
     r0 = seam.take_ready(0)
+    assert r0.precision == "NF4" and r0.needs_decode is False
     stream_c = torch.cuda.current_stream()
     st.stream_wait_event(stream_c, r0.copy_event)
     seam.retire_layer(r0, stream_c)
