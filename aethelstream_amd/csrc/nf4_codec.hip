@@ -568,6 +568,7 @@ static AbsmaxRef absmax_ref(const nf4s_tensor &t) {
   a.q = t.absmax_q;
   a.scale = t.absmax_scale;
   a.group_shift = t.dq_group > 0 ? group_shift(t.dq_group) : 0;
+  a.block_shift = 0;  // the GEMMs' field; the dequant kernels index by block_size
   return a;
 }
 

@@ -265,6 +265,7 @@ struct AbsmaxRef {
   const uint8_t *q;
   const float *scale;
   int32_t group_shift;
+  int32_t block_shift;  // fused GEMMs: log2(block_size / 64) (a block spans 2^shift steps)
 };
 
 __device__ __forceinline__ float load_absmax(const AbsmaxRef &a, int64_t blk) {

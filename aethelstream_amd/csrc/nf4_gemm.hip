@@ -215,11 +215,15 @@ struct FwdStore : HalfTable {
   }
 };
 
-// Forward producer with one load per step and thread (any k % 64 == 0).
+// Forward producer with one load per step and thread (any k % 64 == 0, any
+// block size 64 << s with k % block_size == 0: the block of absolute step t
+// is t >> s, so a step never straddles two blocks and both lanes of a row's
+// 64 elements share one block).
 template <bool kDQ>
 struct FwdProducer : FwdStore, PerStepLoads<kDQ, FwdProducer<kDQ>> {
   const uint8_t *ptr;   // packed bytes of (row, half) at step 0
-  int64_t am_idx;       // absmax block index at step 0
+  int64_t am_row;       // absmax block index of the row's first block
+  int64_t k0;           // absolute step of step 0
   AbsmaxRef am;
   // Tile row r takes W row n0 + r (n0 = the tile's first output column).
   __device__ void init(const GemmArgs &g, int64_t n0, uint32_t b0_lds) {
@@ -228,14 +232,15 @@ struct FwdProducer : FwdStore, PerStepLoads<kDQ, FwdProducer<kDQ>> {
     int64_t n = n0 + row;
     if (n >= g.wn) n = g.wn - 1;  // ragged N: clamp (outputs are not stored)
     ptr = g.packed + n * (g.wk >> 1) + 16 * h + 32 * g.k0;
-    am_idx = n * (g.wk >> 6) + g.k0;
     am = g.am;
+    am_row = n * (g.wk >> (6 + am.block_shift));
+    k0 = g.k0;
   }
   __device__ __forceinline__ void load_step(const GemmArgs &g, int step, u32x4 &w,
                                             AbsRaw &a) const {
     (void)g;
     w = *reinterpret_cast<const u32x4 *>(ptr + (int64_t)step * 32);
-    a = absmax_load<kDQ>(am, am_idx + step);
+    a = absmax_load<kDQ>(am, am_row + ((k0 + step) >> am.block_shift));
   }
 };
 
@@ -455,10 +460,14 @@ struct DgradStore : HalfTable {
 
 // Input-gradient producer with one packed load, one absmax code and one
 // scale load per step and thread (any n % 64 == 0, k % 64 == 0).
+// (Any block size 64 << s with k % block_size == 0: a row's blocks are
+// block_size columns wide, and the two quarters of a 64-column half share a
+// block.)
 template <bool kDQ>
 struct DgradProducer : DgradStore, PerStepLoads<kDQ, DgradProducer<kDQ>> {
   const uint8_t *ptr;
   int64_t am_idx;
+  int64_t am_stride;  // blocks per 64 W rows
   AbsmaxRef am;
   __device__ void init(const GemmArgs &g, int64_t o0, uint32_t b0_lds) {
     (void)b0_lds;
@@ -468,14 +477,16 @@ struct DgradProducer : DgradStore, PerStepLoads<kDQ, DgradProducer<kDQ>> {
     const int64_t cc = col < g.wk ? col : 0;
     const int64_t row = r + 64 * g.k0;  // a split-K slice starts at W row 64 k0
     ptr = g.packed + row * (g.wk >> 1) + (cc >> 1);
-    am_idx = row * (g.wk >> 6) + (cc >> 6);  // absolute block: scale groups stay aligned
     am = g.am;
+    const int bs = 6 + am.block_shift;  // log2(block_size)
+    am_idx = row * (g.wk >> bs) + (cc >> bs);  // absolute block: scale groups stay aligned
+    am_stride = 64 * (g.wk >> bs);
   }
   __device__ __forceinline__ void load_step(const GemmArgs &g, int step, u32x4 &w,
                                             AbsRaw &a) const {
     // Step s covers W rows 64s .. 64s+63.
     w = *reinterpret_cast<const u32x4 *>(ptr + (int64_t)step * 64 * (g.wk >> 1));
-    a = absmax_load<kDQ>(am, am_idx + (int64_t)step * 64 * (g.wk >> 6));
+    a = absmax_load<kDQ>(am, am_idx + (int64_t)step * am_stride);
   }
 };
 
@@ -1486,6 +1497,7 @@ static AbsmaxRef absmax_of(const nf4s_tensor &t) {
   a.q = t.absmax_q;
   a.scale = t.absmax_scale;
   a.group_shift = t.dq_group > 0 ? group_shift(t.dq_group) : 0;
+  a.block_shift = t.block_size > 64 ? group_shift(t.block_size / 64) : 0;
   return a;
 }
 
@@ -1512,12 +1524,19 @@ static int32_t check_gemm(const uint16_t *act, const nf4s_tensor *w, int64_t m, 
                 (long long)wn, (long long)wk);
   const int32_t rc = validate_tensor(w, numel);
   if (rc != NF4S_OK) return rc;
-  if (w->block_size != 64)
-    return fail(NF4S_ERR_UNSUPPORTED_SHAPE, "fused GEMM needs block_size 64, got %d",
-                w->block_size);
+  // A 64-deep reduction step must lie in one absmax block: block sizes 64,
+  // 128, 256, ... (64 << s), with whole blocks per row.
+  const int32_t bsz = w->block_size;
+  if (bsz < 64 || bsz > (1 << 20) || (bsz & (bsz - 1)) != 0)
+    return fail(NF4S_ERR_UNSUPPORTED_SHAPE,
+                "fused GEMM needs block_size 64 << s (64, 128, 256, ...), got %d", bsz);
   if (wk % 64 != 0)
     return fail(NF4S_ERR_UNSUPPORTED_SHAPE, "fused GEMM needs k %% 64 == 0, got %lld",
                 (long long)wk);
+  if (wk % bsz != 0)
+    return fail(NF4S_ERR_UNSUPPORTED_SHAPE,
+                "fused GEMM needs k %% block_size == 0 (whole blocks per row), got k %lld, "
+                "block_size %d", (long long)wk, bsz);
   if (m == 0) return NF4S_OK;
   if (!aligned(act, 16) || !aligned(w->packed, 16))
     return fail(NF4S_ERR_MISALIGNED, "activation and packed weights must be 16-byte aligned");
@@ -1538,7 +1557,7 @@ static int32_t check_offsets(int64_t lda) {
 // groups per row (k % 256), aligned group loads, and 4-block groups inside
 // one double-quant scale.
 static bool fwd_batchable(const nf4s_tensor &w, int64_t k) {
-  if (k % 256 != 0) return false;
+  if (k % 256 != 0 || w.block_size != 64) return false;
   if (w.absmax_q != nullptr) return aligned(w.absmax_q, 4) && w.dq_group >= 4;
   return aligned(w.absmax, 16);
 }
@@ -1816,7 +1835,7 @@ static int32_t gemm_dgrad_groups(const uint16_t *const *dys, const nf4s_tensor *
   // the two blocks of a pair inside one double-quant scale group.
   bool batch = k % 128 == 0;
   for (int32_t i = 0; i < count && batch; ++i) {
-    batch = ns[i] % 256 == 0;
+    batch = ns[i] % 256 == 0 && ws[i].block_size == 64;
     if (dq)
       batch = batch && aligned(ws[i].absmax_q, 2) && ws[i].dq_group >= 2;
     else

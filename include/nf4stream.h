@@ -163,7 +163,10 @@ int32_t nf4s_dequant_batch_bf16(const nf4s_tensor *ts, const int64_t *ns,
  * Replaces matmul_tb (doublepass/src/math.rs:9-21) at its call sites in
  * single_layer_forward (doublepass/src/forward.rs:174-176,244,251-252,255) and
  * the recompute forward (doublepass/src/backward.rs:447-451).
- * Requires k % 64 == 0, block_size == 64, x/y 16-byte aligned.  Every GEMM
+ * Requires k % 64 == 0, block_size 64 << s (64 as the reference writes,
+ * or 128, 256, ...; shard_engine/src/index.rs:33 lets the index name any)
+ * with k % block_size == 0, x/y 16-byte aligned.  Block sizes above 64 run
+ * the per-step weight loads (64 takes the batched ones).  Every GEMM
  * entry point takes m, n and k up to 2^39 (tile counts are 32-bit; the launch
  * also bounds the total of output tiles by 2^31 - 1) and rejects larger ones
  * with NF4S_ERR_UNSUPPORTED_SHAPE.
@@ -176,7 +179,8 @@ int32_t nf4s_gemm_fwd(const uint16_t *x, const nf4s_tensor *w, int64_t m,
  * W the NF4 tensor of shape [n,k], fp32 accumulation.
  * Replaces the dY.W loops of single_layer_backward
  * (doublepass/src/backward.rs:79-85,117-129,160-168,284-300).
- * Requires n % 64 == 0, k % 64 == 0, block_size == 64.
+ * Requires n % 64 == 0, k % 64 == 0, block_size 64 << s with
+ * k % block_size == 0 (as nf4s_gemm_fwd).
  */
 int32_t nf4s_gemm_dgrad(const uint16_t *dy, const nf4s_tensor *w, int64_t m,
                         int64_t n, int64_t k, uint16_t *dx, void *stream);
