@@ -45,4 +45,18 @@ inline int32_t group_shift(int32_t group) {
 // pointer and double-quant fields.
 int32_t validate_tensor(const nf4s_tensor *t, int64_t n);
 
+// The grouped forward GEMM of nf4_gemm.hip, for the no-allocation entry point
+// in nf4_noalloc.hip.  fwd_workspace_query checks count and ns and sets
+// *bytes to the split-K workspace that nf4s_gemm_fwd_grouped_ws would use
+// (nf4s_gemm_fwd_workspace_size); gemm_fwd_grouped_on runs that entry
+// point's launches on the given workspace.
+int32_t fwd_workspace_query(const int64_t *ns, int32_t count, int64_t m, int64_t k,
+                            int64_t *bytes);
+int32_t gemm_fwd_grouped_on(const uint16_t *x, const nf4s_tensor *ws, const int64_t *ns,
+                            uint16_t *const *ys, int32_t count, int64_t m, int64_t k,
+                            hipStream_t s, void *work, int64_t work_bytes);
+// One split-K partial tile of the forward GEMM: 256 threads x 256 fp32
+// accumulators (a 512 x 128 output tile).
+constexpr int64_t kGemmPartialTileBytes = 256 * 256 * 4;
+
 }  // namespace nf4s

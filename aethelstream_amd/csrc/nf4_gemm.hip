@@ -1874,27 +1874,23 @@ static int64_t fwd_workspace_bytes(const int64_t *ns, int32_t count, int64_t m, 
   return best;
 }
 
-// Split-K workspace of nf4s_gemm_fwd_grouped_noalloc: a file-scope device
-// array, one copy per GPU, held until the process ends.  A plan never needs
-// more partial tiles than the device has CUs (S <= CUs / r slices for r tail
-// tiles), so 256 partial tiles (64 MiB) cover every shape on a 256-CU MI355X.
-constexpr int64_t kScratchTiles = 256;
-constexpr int64_t kScratchBytes = kScratchTiles * kPartialFloats * (int64_t)sizeof(float);
-static __device__ __align__(256) float scratch[kScratchTiles * kPartialFloats];
+static_assert(kPartialFloats * (int64_t)sizeof(float) == kGemmPartialTileBytes,
+              "partial tile size shared with nf4_noalloc.hip");
 
-// Device address of the current GPU's `scratch`, looked up on every call
-// with that device current: each GPU holds its own copy at its own address,
-// and a hipDeviceReset reloads the code object (a cached address would then
-// dangle).  The lookup is a host-side table query, small next to a GEMM
-// launch.  The host-side name is only a stand-in handle: kernels get this
-// address, never the name.
-static int32_t scratch_on_current_device(void **out) {
-  void *p = nullptr;
-  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-  if (e != hipSuccess || p == nullptr)
-    return fail(NF4S_ERR_HIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
-  *out = p;
+int32_t fwd_workspace_query(const int64_t *ns, int32_t count, int64_t m, int64_t k,
+                            int64_t *bytes) {
+  if (bytes == nullptr) return fail(NF4S_ERR_INVALID_ARGUMENT, "bytes is NULL");
+  *bytes = 0;
+  if (count <= 0 || count > kMaxGroups || ns == nullptr)
+    return fail(NF4S_ERR_INVALID_ARGUMENT, "count must be 1..%d with sizes", kMaxGroups);
+  *bytes = fwd_workspace_bytes(ns, count, m, k);
   return NF4S_OK;
+}
+
+int32_t gemm_fwd_grouped_on(const uint16_t *x, const nf4s_tensor *ws, const int64_t *ns,
+                            uint16_t *const *ys, int32_t count, int64_t m, int64_t k,
+                            hipStream_t s, void *work, int64_t work_bytes) {
+  return gemm_fwd_groups(x, ws, ns, ys, count, m, k, s, work, work_bytes);
 }
 
 }  // namespace nf4s
@@ -1942,32 +1938,7 @@ int32_t nf4s_gemm_fwd_grouped_ws(const uint16_t *x, const nf4s_tensor *ws, const
 int32_t nf4s_gemm_fwd_workspace_size(const int64_t *ns, int32_t count, int64_t m, int64_t k,
                                      int64_t *bytes) {
   clear_error();
-  if (bytes == nullptr) return fail(NF4S_ERR_INVALID_ARGUMENT, "bytes is NULL");
-  *bytes = 0;
-  if (count <= 0 || count > kMaxGroups || ns == nullptr)
-    return fail(NF4S_ERR_INVALID_ARGUMENT, "count must be 1..%d with sizes", kMaxGroups);
-  *bytes = fwd_workspace_bytes(ns, count, m, k);
-  return NF4S_OK;
-}
-
-// nf4s_gemm_fwd_grouped_ws with the library's static per-GPU scratch as the
-// workspace: no allocation, for callers that cannot allocate.
-int32_t nf4s_gemm_fwd_grouped_noalloc(const uint16_t *x, const nf4s_tensor *ws, const int64_t *ns,
-                                      uint16_t *const *ys, int32_t count, int64_t m, int64_t k,
-                                      void *stream) {
-  clear_error();
-  if (count <= 0 || count > kMaxGroups || ns == nullptr)
-    return fail(NF4S_ERR_INVALID_ARGUMENT, "count must be 1..%d with sizes", kMaxGroups);
-  const int64_t need = fwd_workspace_bytes(ns, count, m, k);
-  if (need > kScratchBytes)
-    return fail(NF4S_ERR_UNSUPPORTED_SHAPE,
-                "split-K workspace of %lld bytes exceeds the static scratch of %lld bytes; "
-                "use nf4s_gemm_fwd_grouped_ws with a workspace of that size",
-                (long long)need, (long long)kScratchBytes);
-  void *p = nullptr;
-  const int32_t rc = scratch_on_current_device(&p);
-  if (rc != NF4S_OK) return rc;
-  return gemm_fwd_groups(x, ws, ns, ys, count, m, k, as_stream(stream), p, kScratchBytes);
+  return fwd_workspace_query(ns, count, m, k, bytes);
 }
 
 int32_t nf4s_gemm_fwd_swiglu(const uint16_t *x, const nf4s_tensor *w_gate,

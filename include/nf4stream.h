@@ -273,9 +273,11 @@ int32_t nf4s_gemm_fwd_workspace_size(const int64_t *ns, int32_t count, int64_t m
 
 /*
  * nf4s_gemm_fwd_grouped_ws whose split-K workspace is the library's own
- * static device array (64 MiB per GPU, allocated with the code object and
- * held until the process ends) instead of a caller buffer: this call
- * allocates nothing, ever.  No counterpart in the reference: it is for
+ * static device array (64 MiB per GPU) instead of a caller buffer: this call
+ * allocates nothing, ever.  The array is reserved on a GPU by the first call
+ * of this entry point there (with the code object that holds it) and held
+ * until the process ends; a process that never calls it holds none of it.
+ * No counterpart in the reference: it is for
  * callers that cannot allocate (code under HIP graph capture, tight serving
  * loops, harnesses that forbid hipMalloc).  Fails with
  * NF4S_ERR_UNSUPPORTED_SHAPE when the split needs more than the array holds
@@ -284,10 +286,10 @@ int32_t nf4s_gemm_fwd_workspace_size(const int64_t *ns, int32_t count, int64_t m
  * without ordering, or several host threads) race.  Results are bit-identical
  * to nf4s_gemm_fwd_grouped_ws with a large enough workspace.  The array's
  * device address is looked up on every call (valid across hipDeviceReset).
- * Under HIP graph capture: make one call on the device (of any entry point)
- * before capturing, so that the library's code object is already loaded
- * there; the call itself issues only kernel launches (no memset), so a
- * captured call replays correctly.
+ * Under HIP graph capture: make one call of this entry point on the device
+ * before capturing, so that the code objects of the array and of the GEMM
+ * kernels are already loaded there; the call itself issues only kernel
+ * launches (no memset), so a captured call replays correctly.
  */
 int32_t nf4s_gemm_fwd_grouped_noalloc(const uint16_t *x, const nf4s_tensor *ws,
                                       const int64_t *ns, uint16_t *const *ys,

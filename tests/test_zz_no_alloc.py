@@ -4,6 +4,9 @@ both through the C ABI: bit-identical outputs on two calls in a row, the
 second smaller, so stale partials of the first call would show in the second.
 """
 import ctypes
+import os
+import subprocess
+import sys
 
 import pytest
 import torch
@@ -123,3 +126,43 @@ def test_noalloc_captured_in_a_graph_replays_bit_exact():
         for a, b in zip(outs, ref):
             assert not torch.isnan(a).any(), f"replay {rep} left outputs unwritten"
             assert torch.equal(a, b), f"replay {rep} differs from the eager call"
+
+
+_RESERVE_PROBE = r"""
+import ctypes, sys, torch
+sys.path.insert(0, sys.argv[1])
+from aethelstream_amd import _lib, gemm, nf4
+def free():
+    torch.cuda.synchronize()
+    return torch.cuda.mem_get_info()[0]
+lib = _lib.load()
+w = nf4.quantize_weight(torch.randn(640, 8192, device="cuda") * 0.02, double_quant=True)
+x = torch.randn(512, 8192, device="cuda").to(torch.bfloat16)
+y = torch.empty(512, 640, dtype=torch.bfloat16, device="cuda")
+gemm.linear_fwd(x, w)
+gemm.linear_dgrad(torch.randn(512, 640, device="cuda").to(torch.bfloat16), w)
+f0 = free()
+d = (_lib.Nf4sTensor * 1)(w.descriptor())
+ns = (ctypes.c_int64 * 1)(640)
+ys = (ctypes.c_void_p * 1)(y.data_ptr())
+_lib.check(lib.nf4s_gemm_fwd_grouped_noalloc(x.data_ptr(), d, ns, ys, 1, 512, 8192,
+                                             torch.cuda.current_stream().cuda_stream))
+f1 = free()
+print(f0 - f1)
+"""
+
+
+def test_scratch_reserved_only_by_the_noalloc_entry_point():
+    """The 64 MiB array lives in a code object of its own, which HIP loads on
+    a GPU at its first use there.  In a fresh process the other GEMM entry
+    points (forward with split-K, input gradient) leave it unreserved, and
+    the first no-allocation call reserves it: device free memory drops by at
+    least 64 MiB across that call alone (its outputs and inputs exist
+    before)."""
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    print("fresh process: GEMM calls, then the first noalloc call", flush=True)
+    r = subprocess.run([sys.executable, "-c", _RESERVE_PROBE, root], capture_output=True,
+                       text=True, timeout=300)
+    assert r.returncode == 0, r.stderr[-2000:]
+    dropped = int(r.stdout.strip().splitlines()[-1])
+    assert dropped >= 64 << 20, f"first noalloc call reserved only {dropped} bytes"
