@@ -401,7 +401,8 @@ int32_t nf4s_take_ready(nf4s_dbuf *d, uint32_t layer_idx, const void *pinned,
  * Residency table: the layers whose blobs a prefetcher has made resident in
  * pinned host memory, the ready map of FlowCast's prefetch state machine
  * (flowcast/src/state_machine.rs:306-346 is_ready / take_slot).  Host-only
- * and thread-safe: one thread may publish while another waits.
+ * and thread-safe: one thread may publish while another waits.  Destroy it
+ * only when no other thread uses it.
  */
 typedef struct nf4s_residency nf4s_residency;
 int32_t nf4s_residency_create(uint32_t num_layers, nf4s_residency **out);
@@ -424,7 +425,9 @@ int32_t nf4s_residency_wait(nf4s_residency *r, uint32_t layer_idx,
 /* FlowCast::take_ready (flowcast/src/lib.rs:458-498) in full:
  * nf4s_residency_wait, then nf4s_dbuf_advance of the taken blob.  The
  * ReadyLayer carries the published precision and needs_decode =
- * (precision is INT4 or INT8), as QuantizedDecoder::needs_decode. */
+ * (precision is INT4 or INT8), as QuantizedDecoder::needs_decode.  A layer
+ * whose copy then fails (capacity, unreleased slot) stays taken, as the
+ * reference drops the taken slot when its advance fails. */
 int32_t nf4s_take_ready_wait(nf4s_dbuf *d, nf4s_residency *r, uint32_t layer_idx,
                              int64_t timeout_us, nf4s_ready_layer *out);
 
