@@ -1,4 +1,5 @@
 """Streamed layer stack (flowcast VramDoubleBuffer semantics) on the GPU."""
+import ctypes
 import threading
 import time
 
@@ -74,6 +75,37 @@ def test_slot_reuse_invariant_and_capacity_error():
     with pytest.raises(_lib.Nf4sError, match="not a slot"):
         dbuf.release(pb.ptr, stream)
     torch.cuda.synchronize()
+    dbuf.close()
+    pb.close()
+
+
+def test_take_ready_wait_failed_copy_leaves_layer_taken():
+    """nf4s_take_ready_wait takes the layer from the residency table before
+    it issues the copy; a copy that fails (here a blob larger than the slot,
+    vram_double_buffer.rs:269-275) returns the copy's error, and the layer
+    stays taken, as the reference's take_ready drops the taken slot when its
+    advance fails (flowcast/src/lib.rs:460-476): a second wait misses until
+    the layer is published again, and the table itself stays usable."""
+    layout = st.LayerLayout(SHAPES)
+    pb = st.PinnedBuffer(layout.nbytes + 64)
+    dbuf = st.VramDoubleBuffer(layout.nbytes)
+    res = st.Residency(2)
+    lib = _lib.load()
+    out = _lib.Nf4sReadyLayer()
+    res.publish(1, pb.ptr, layout.nbytes + 64, st.PRECISION_NF4)
+    rc = lib.nf4s_take_ready_wait(dbuf.handle, res.handle, 1, 100000, ctypes.byref(out))
+    assert rc == 1 and b"exceeds slot capacity" in lib.nf4s_last_error_message()
+    with pytest.raises(st.PrefetchMiss, match="prefetch miss on layer 1"):
+        res.wait(1, 0.02)
+    res.publish(1, pb.ptr, layout.nbytes, st.PRECISION_NF4)
+    _lib.check(lib.nf4s_take_ready_wait(dbuf.handle, res.handle, 1, 100000, ctypes.byref(out)))
+    assert out.layer_idx == 1 and out.bytes == layout.nbytes
+    assert out.precision == st.PRECISION_NF4 and out.needs_decode == 0
+    stream = torch.cuda.current_stream()
+    _lib.check(lib.nf4s_retire_layer(dbuf.handle, ctypes.byref(out),
+                                     ctypes.c_void_p(stream.cuda_stream)))
+    torch.cuda.synchronize()
+    res.close()
     dbuf.close()
     pb.close()
 
