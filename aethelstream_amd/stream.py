@@ -221,6 +221,13 @@ class PrefetchMiss(Exception):
         self.layer_idx = layer_idx
 
 
+def _timeout_us(timeout: float) -> int:
+    """Seconds as the ABI's int64 microseconds; an infinite timeout (wait
+    until published) becomes 10^12 s, negative ones are passed on for the
+    library to reject."""
+    return int(min(float(timeout), 1e12) * 1e6)
+
+
 class Residency:
     """The ready map of FlowCast's prefetch state machine
     (flowcast/src/state_machine.rs:306-346): layers a prefetcher published as
@@ -242,7 +249,7 @@ class Residency:
         reference checks the deadline first)."""
         p, nb, pr = ctypes.c_void_p(), ctypes.c_int64(), ctypes.c_int32()
         lib = _lib.load()
-        rc = lib.nf4s_residency_wait(self.handle, int(layer_idx), int(timeout * 1e6),
+        rc = lib.nf4s_residency_wait(self.handle, int(layer_idx), _timeout_us(timeout),
                                      ctypes.byref(p), ctypes.byref(nb), ctypes.byref(pr))
         if rc == NF4S_ERR_PREFETCH_MISS:
             raise PrefetchMiss(layer_idx, lib.nf4s_last_error_message().decode())
@@ -331,7 +338,7 @@ class FlowCastSeam:
         raw = _lib.Nf4sReadyLayer()
         lib = _lib.load()
         rc = lib.nf4s_take_ready_wait(self.dbuf.handle, self.residency.handle, layer_idx,
-                                      int(timeout * 1e6), ctypes.byref(raw))
+                                      _timeout_us(timeout), ctypes.byref(raw))
         if rc == NF4S_ERR_PREFETCH_MISS:
             raise PrefetchMiss(layer_idx, lib.nf4s_last_error_message().decode())
         _lib.check(rc)

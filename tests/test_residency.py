@@ -85,3 +85,15 @@ def test_rejections():
     assert lib.nf4s_take_ready_wait(None, r.handle, 0, 1000, ctypes.byref(out)) == 1
     assert lib.nf4s_strerror(12) == b"prefetch miss"
     r.close()
+
+
+def test_infinite_timeout_waits_for_the_publish():
+    # float("inf") means "until published": the binding caps it at 10^12 s.
+    r = _table(1)
+    th = threading.Thread(target=lambda: (time.sleep(0.03), r.publish(0, PTR, 8, st.PRECISION_NF4)))
+    th.start()
+    assert r.wait(0, float("inf")) == (PTR, 8, st.PRECISION_NF4)
+    th.join()
+    with pytest.raises(_lib.Nf4sError, match="negative timeout"):
+        r.wait(0, -1.0)
+    r.close()
