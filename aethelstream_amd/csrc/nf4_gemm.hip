@@ -632,8 +632,8 @@ __device__ __forceinline__ void read_frag(const Producer &prod, const u32x4 *__r
 //      current buffer once this wave's reads of it have returned
 //   .  the MFMA alone
 // Each slot holds about the issue time of one MFMA (32 cycles), and an MFMA
-// hides about 5 independent VALU instructions: the table's 16 products go
-// in 4 slots of 3-5 instructions.  The last weight-tile store (word 3's W
+// hides about 5 independent VALU instructions: the 8 products of this lane's
+// half of the table go in 4 slots of 3-5 instructions.  The last weight-tile store (word 3's W
 // stage 5) sits at slot 44, 11 slots before the barrier, whose lgkmcnt(0)
 // must see it complete; the A jobs follow in the last slots, after a wait
 // for this wave's fragment reads only (the LDS queue is in order, so the
