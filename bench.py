@@ -626,12 +626,17 @@ def bench_stream(torch, nf4, gemm, nlayers, M=4096):
         gemm.linear_fwd_grouped(x, views[4:6], outs[4:6])
         gemm.linear_fwd(hid, views[6], outs[6])
 
-    def wall(fn):
+    def wall(fn, name):
+        # A marker range per phase, so a kernel + memory-copy trace can
+        # attribute the copies and the GEMMs to it.
         torch.cuda.synchronize()
+        torch.cuda.nvtx.range_push(name)
         t = time.perf_counter()
         fn()
         torch.cuda.synchronize()
-        return time.perf_counter() - t
+        t = time.perf_counter() - t
+        torch.cuda.nvtx.range_pop()
+        return t
 
     def copies_only():
         for l in range(nlayers):
@@ -648,10 +653,10 @@ def bench_stream(torch, nf4, gemm, nlayers, M=4096):
     def streamed():
         st.run_stack(host, layout, dbuf, compute, comp)
 
-    wall(streamed)                      # warm-up
-    t_h2d = wall(copies_only)
-    t_comp = wall(compute_only)
-    t_tot = wall(streamed)
+    wall(streamed, "config5_warmup")
+    t_h2d = wall(copies_only, "config5_copies_only")
+    t_comp = wall(compute_only, "config5_compute_only")
+    t_tot = wall(streamed, "config5_streamed")
     last = [o.clone() for o in outs]
     compute(nlayers - 1, rviews)
     torch.cuda.synchronize()
