@@ -250,6 +250,10 @@ int32_t nf4s_residency_wait(nf4s_residency *r, uint32_t layer_idx, int64_t timeo
   if (r == nullptr || pinned == nullptr || bytes == nullptr || precision == nullptr)
     return fail(NF4S_ERR_INVALID_ARGUMENT, "bad residency_wait args");
   if (timeout_us < 0) return fail(NF4S_ERR_INVALID_ARGUMENT, "negative timeout");
+  // steady_clock counts int64 nanoseconds: longer timeouts (about 31 years
+  // and up) wait as long as 10^15 us, so the deadline cannot overflow.
+  constexpr int64_t kMaxTimeoutUs = (int64_t)1000000000000000;
+  if (timeout_us > kMaxTimeoutUs) timeout_us = kMaxTimeoutUs;
   using clock = std::chrono::steady_clock;
   const clock::time_point start = clock::now();
   const clock::time_point deadline = start + std::chrono::microseconds(timeout_us);

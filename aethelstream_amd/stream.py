@@ -223,9 +223,9 @@ class PrefetchMiss(Exception):
 
 def _timeout_us(timeout: float) -> int:
     """Seconds as the ABI's int64 microseconds; an infinite timeout (wait
-    until published) becomes 10^12 s, negative ones are passed on for the
+    until published) becomes 10^9 s, negative ones are passed on for the
     library to reject."""
-    return int(min(float(timeout), 1e12) * 1e6)
+    return int(min(float(timeout), 1e9) * 1e6)
 
 
 class Residency:

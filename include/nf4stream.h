@@ -417,7 +417,8 @@ int32_t nf4s_residency_publish(nf4s_residency *r, uint32_t layer_idx,
  * layer is resident, then takes it (a second wait for it waits for the next
  * publish).  As the reference, the deadline is checked before readiness, so
  * timeout_us = 0 always misses; past the deadline it returns
- * NF4S_ERR_PREFETCH_MISS with the message "prefetch miss on layer N". */
+ * NF4S_ERR_PREFETCH_MISS with the message "prefetch miss on layer N".
+ * Timeouts above 10^15 us (about 31 years) wait that long. */
 int32_t nf4s_residency_wait(nf4s_residency *r, uint32_t layer_idx,
                             int64_t timeout_us, const void **pinned,
                             int64_t *bytes, int32_t *precision);

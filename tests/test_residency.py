@@ -88,7 +88,7 @@ def test_rejections():
 
 
 def test_infinite_timeout_waits_for_the_publish():
-    # float("inf") means "until published": the binding caps it at 10^12 s.
+    # float("inf") means "until published": the binding caps it at 10^9 s.
     r = _table(1)
     th = threading.Thread(target=lambda: (time.sleep(0.03), r.publish(0, PTR, 8, st.PRECISION_NF4)))
     th.start()
@@ -96,4 +96,17 @@ def test_infinite_timeout_waits_for_the_publish():
     th.join()
     with pytest.raises(_lib.Nf4sError, match="negative timeout"):
         r.wait(0, -1.0)
+    r.close()
+
+
+def test_huge_timeout_does_not_overflow_the_deadline():
+    # INT64_MAX microseconds would overflow a nanosecond deadline; the table
+    # clamps it, so a resident layer is still taken and not a miss.
+    r = _table(1)
+    r.publish(0, PTR, 4, st.PRECISION_NF4)
+    lib = _lib.load()
+    p, nb, pr = ctypes.c_void_p(), ctypes.c_int64(), ctypes.c_int32()
+    assert lib.nf4s_residency_wait(r.handle, 0, 2**63 - 1, ctypes.byref(p), ctypes.byref(nb),
+                                   ctypes.byref(pr)) == 0
+    assert (p.value, nb.value) == (PTR, 4)
     r.close()
