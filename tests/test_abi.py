@@ -151,6 +151,13 @@ def test_fwd_workspace_size_query():
                                         None) == _lib.NF4S_ERR_INVALID_ARGUMENT
     assert lib.nf4s_gemm_fwd_grouped_ws(0x1000, None, ns, None, 1, 64, 64, 0x1008, 64,
                                         None) == _lib.NF4S_ERR_MISALIGNED
+    # The no-allocation entry point checks count and sizes before it looks up
+    # (and so loads) its static scratch: no GPU call is reached here.
+    na = lib.nf4s_gemm_fwd_grouped_noalloc
+    assert na(0x1000, None, ns, None, 0, 64, 64, None) == _lib.NF4S_ERR_INVALID_ARGUMENT
+    assert na(0x1000, None, ns, None, 5, 64, 64, None) == _lib.NF4S_ERR_INVALID_ARGUMENT
+    assert na(0x1000, None, None, None, 1, 64, 64, None) == _lib.NF4S_ERR_INVALID_ARGUMENT
+    assert b"count must be 1..4" in lib.nf4s_last_error_message()
 
 
 def torch_has_gpu():
